@@ -1,0 +1,129 @@
+/*
+ * tmoe.h — C ABI of libtmoe, the MI355X (gfx950) MoE-layer hot path.
+ *
+ * Conventions
+ *   - Every pointer argument named x/out/ids/weights/... is a DEVICE pointer
+ *     unless stated otherwise; sizes are plain ints.  bf16 tensors are passed as
+ *     void* holding IEEE bfloat16 bit patterns, row-major, contiguous.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Calls are asynchronous on `stream`; the return value reports argument
+ *     validation and launch errors only (0 = TMOE_OK, negative = tmoe_status).
+ *     Conditions the device detects (an expert id outside [0, E]) are recorded
+ *     in the workspace and reported by tmoe_workspace_status().
+ *   - Nothing here allocates device memory.  Callers pass a workspace of at
+ *     least tmoe_workspace_bytes(...) bytes, ZERO-FILLED before its first use;
+ *     the kernels leave its counters zeroed again.  Calls that share one
+ *     workspace must be ordered (same stream, or joined with events).
+ *   - Expert weights are reached through a device "expert table":
+ *       bf16 table  uint64_t[E][2] = { gate_up [2I, H], down [H, I] } base pointers
+ *       int4 table  uint64_t[E][4] = { gate_up packed [2I, H/2] u8, gate_up scales
+ *                                      [2I, H/G] bf16, down packed [H, I/2] u8,
+ *                                      down scales [H, I/G] bf16 }
+ *     so expert ids never leave the device (no per-layer host sync, the
+ *     reference's `top_k_index[0].tolist()` at tarfa/engine/fused_int4.py:166).
+ *
+ * Reference citations are into syncroot/tarfa (tarfa/...) and the transformers
+ * 5.15.0 Qwen3.5-MoE modelling file it calls (transformers/...).
+ */
+#ifndef TMOE_H
+#define TMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMOE_ABI_VERSION 1
+
+enum tmoe_status {
+  TMOE_OK = 0,
+  TMOE_ERR_NULL = -1,       /* a required pointer is NULL                          */
+  TMOE_ERR_SHAPE = -2,      /* unsupported or inconsistent sizes                   */
+  TMOE_ERR_ALIGN = -3,      /* a pointer is not 16-byte aligned                    */
+  TMOE_ERR_WORKSPACE = -4,  /* workspace smaller than tmoe_workspace_bytes()       */
+  TMOE_ERR_HIP = -5,        /* a HIP runtime call or kernel launch failed          */
+  TMOE_ERR_EXPERT_ID = -6,  /* device saw an expert id outside [0, E] (sentinel E is skipped) */
+};
+
+/* ABI version of the loaded library (TMOE_ABI_VERSION at build time). */
+int tmoe_abi_version(void);
+
+/* Static text for a status code. */
+const char* tmoe_strerror(int status);
+
+/* Workspace bytes needed by any entry point below for T tokens at this shape
+ * (Is = shared-expert intermediate size, 0 = no shared expert). */
+size_t tmoe_workspace_bytes(int T, int H, int E, int I, int k, int Is);
+
+/* Synchronise `stream`, then return and clear the device-side status the
+ * kernels recorded in `workspace` (TMOE_OK or TMOE_ERR_EXPERT_ID). */
+int tmoe_workspace_status(void* workspace, void* stream);
+
+/* ---------------------------------------------------------------- seeded data
+ * Counter-based generator (splitmix64 output function over key + (i+1)*golden,
+ * Irwin-Hall n=4 normal).  Stands in for the reference's seeded torch.randn
+ * (tarfa/engine/moe_kernel.py:129-139) so any expert can be regenerated on the
+ * host bit-identically.
+ *   fill_bf16: dst[i] = bf16(fp32(c16(h_{start+i})) * scale)        (weights, activations)
+ *   fill_f32 : dst[i] = fp32(double(c32(h_{2(start+i)}, h_{2(start+i)+1})) * scale)  (logits)
+ */
+int tmoe_fill_bf16(void* dst, uint64_t n, uint64_t key, float scale, uint64_t start, void* stream);
+int tmoe_fill_f32(float* dst, uint64_t n, uint64_t key, double scale, uint64_t start, void* stream);
+
+/* ---------------------------------------------------------------- router (a1)
+ * Replaces Qwen3_5MoeTopKRouter.forward (transformers/.../modeling_qwen3_5_moe.py:768-776)
+ * with fp32 logits: logits = x . router_w^T in fp32 (or `logits_in` when not NULL,
+ * then x/router_w may be NULL), softmax in fp32, top-k by logit descending with
+ * ties to the lower expert index, renormalised in fp32, weights cast to bf16.
+ * ids_out [T,k] int64, weights_out [T,k] bf16, logits_out [T,E] fp32 (optional),
+ * heat [E] uint32 (optional): heat[e] += 1 per selection (residency ledger).
+ */
+int tmoe_router_topk(const void* x, const void* router_w, const float* logits_in, int T, int H,
+                     int E, int k, int64_t* ids_out, void* weights_out, float* logits_out,
+                     uint32_t* heat, void* stream);
+
+/* ---------------------------------------------------------------- dispatch (a3)
+ * Token -> expert permutation of the reference's prefill
+ * (tarfa/engine/fused_int4.py:228-229, 241): rows grouped by ascending expert id,
+ * within an expert in (slot, token) order.  offsets [E+1] int32, perm [T*k] int32
+ * with perm[r] = t*k + slot (entries past offsets[E] are unused); inv [T*k] int32
+ * with inv[t*k + slot] = r (-1 for skipped ids).  Ids outside [0, E) are skipped.
+ */
+int tmoe_dispatch(const int64_t* ids, int T, int k, int E, int32_t* offsets, int32_t* perm,
+                  int32_t* inv, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------- experts.forward (a2-a7)
+ * Drop-in for the routed-compute step `experts.forward(hidden_states, top_k_index,
+ * top_k_weights)` that the reference installs with types.MethodType
+ * (tarfa/engine/fused_int4.py:155-262; same boundary channel.py:44-61).
+ * x [T,H] bf16, ids [T,k] int64 (sentinel E skipped), weights [T,k] bf16, out [T,H] bf16.
+ *   T == 1: per routed expert in router order, bf16(F.linear(bf16(silu(g))*u, Wd)),
+ *           acc = bf16(acc + bf16(w_j * d_j))                (fused_int4.py:192-194)
+ *   T  > 1: dispatch, grouped GEMM, and per token bf16 adds in ascending expert id
+ *           (index_add_, fused_int4.py:239-244)
+ */
+int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
+                              const uint64_t* expert_table, int H, int E, int I, int k, void* out,
+                              void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------- whole MoE block (a1-a8)
+ * Replaces Qwen3_5MoeSparseMoeBlock.forward (transformers/.../modeling_qwen3_5_moe.py:787-798)
+ * with the experts step above: router (fp32 logits), routed experts, shared expert
+ * bf16(sigmoid(bf16(x.w_sg)) * down(bf16(silu(bf16(gate x))) * bf16(up x))), and
+ * out = bf16(routed + shared).  router_w may be NULL when logits_in [T,E] fp32 is given;
+ * the four shared pointers may all be NULL (Is = 0) for a layer without a shared expert.
+ * ids_out / weights_out (optional) receive the routing; heat as in tmoe_router_topk.
+ */
+int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,
+                        const uint64_t* expert_table, const void* sh_gate, const void* sh_up,
+                        const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k,
+                        int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                        void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMOE_H */

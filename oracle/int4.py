@@ -1,0 +1,91 @@
+"""Int4 fast mode, CPU restatement (oracle, test infrastructure only).
+
+Format (group-quantised variant of the reference's per-row format,
+tarfa/engine/moe_kernel.py:10-14, tarfa/engine/channel_q4.py:10-14):
+
+  packed [N, K/2] uint8   low nibble = even k, high nibble = odd k, value = nibble - 8
+  scales [N, K/G] bf16    one scale per (row, group of G consecutive k)
+  dequant  w_hat = bf16(fp32((nibble - 8) * s[n, k // G]))   (the product is exact in
+           fp32: at most 3 x 8 significant bits; only the bf16 rounding is inexact)
+
+The reference carries no quantiser (its int4 files come from outside the
+repository, channel_q4.py:6).  The quantiser here is this build's definition:
+
+  s = bf16(fp32(max_{k in group} |w| / 7))      fp32 IEEE division, then RNE to bf16
+  q = clamp(rint(fp32(w / s)), -8, 7)           rint = round half to even; s == 0 -> q = 0
+"""
+import numpy as np
+
+from . import bf16
+
+rb = bf16.rnd
+
+
+def quantize(w, group=128):
+    """bf16 weights [N,K] (fp32 values) -> (packed [N,K/2] uint8, scale bf16 bits [N,K/G] uint16)."""
+    w = np.asarray(w, np.float32)
+    N, K = w.shape
+    assert K % group == 0 and group % 2 == 0
+    wg = w.reshape(N, K // group, group)
+    amax = np.abs(wg).max(axis=-1)
+    s = rb(amax / np.float32(7.0))                            # fp32 division, RNE to bf16
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = wg / s[..., None]                                  # fp32 / fp32, IEEE
+    q = np.where(s[..., None] == 0, 0.0, np.rint(r))
+    q = np.clip(q, -8, 7).astype(np.int32).reshape(N, K)
+    nib = (q + 8).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << np.uint8(4))).astype(np.uint8)
+    return packed, bf16.bits(s)
+
+
+def codes(packed):
+    """packed [N,K/2] -> signed codes [N,K] int32 (even k = low nibble)."""
+    p = np.asarray(packed, np.uint8)
+    lo = (p & 0xF).astype(np.int32) - 8
+    hi = (p >> 4).astype(np.int32) - 8
+    return np.stack([lo, hi], axis=-1).reshape(p.shape[0], -1)
+
+
+def dequant(packed, scale_bits, group=128):
+    """(packed, bf16 scale bits) -> dequantised bf16 bit patterns [N,K] (uint16).
+
+    Restates channel_q4.py:10-14 / moe_kernel.py:110-114 (``q.to(dtype) * scale``)
+    with a per-group instead of a per-row scale.
+    """
+    q = codes(packed).astype(np.float32)
+    s = np.repeat(bf16.to_f32(scale_bits), group, axis=-1)
+    with np.errstate(over="ignore"):                 # huge scales overflow to inf, as torch does
+        return bf16.bits(q * s)
+
+
+def gemv_f32(packed, scale_bits, x, group=128):
+    """fp32 sum over groups of s[n,g] * sum_{k in g} q[n,k] x[k] (fp64 inside, fp32 out).
+
+    The Triton kernel folds the per-row scale onto the fp32 dot
+    (moe_kernel.py:60-63); with group scales the fold happens per group.
+    """
+    q = codes(packed).astype(np.float64)
+    N, K = q.shape
+    s = bf16.to_f32(scale_bits).astype(np.float64)
+    part = (q.reshape(N, K // group, group) * np.asarray(x, np.float64).reshape(1, K // group, group)).sum(-1)
+    return (part * s).sum(-1).astype(np.float32)
+
+
+def ffn(x, experts, rw, group=128):
+    """Labelled fast mode for one token: moe_kernel.py:90-104 with group scales.
+
+    ``experts`` = list of (gate_up_packed, gate_up_scale, down_packed, down_scale)
+    in router order; ``rw`` the bf16 routing weights.  Up projection in fp32,
+    ``act = bf16(silu(g) * u)`` in fp32 (``:100``), down projection in fp32, then the
+    fp32 weighted sum over experts (``:103``) and one cast to bf16 (``:104``).
+    """
+    x = np.asarray(x, np.float32)
+    y = np.zeros(x.shape[0], np.float64)
+    for (gq, gs, dq, ds), w in zip(experts, np.asarray(rw, np.float32).reshape(-1)):
+        gu = gemv_f32(gq, gs, x, group).astype(np.float64)
+        inter = gu.shape[0] // 2
+        g, u = gu[:inter], gu[inter:]
+        act = rb(((g / (1.0 + np.exp(-g))).astype(np.float32).astype(np.float64) * u).astype(np.float32))
+        d = gemv_f32(dq, ds, act, group).astype(np.float64)
+        y = (y + (d * np.float64(w)).astype(np.float32)).astype(np.float32).astype(np.float64)
+    return rb(y.astype(np.float32))

@@ -1,0 +1,105 @@
+"""Counter-based seeded generator, numpy restatement (oracle, test infrastructure only).
+
+The reference seeds its known-answer test with ``torch.manual_seed(0)`` and
+``torch.randn`` (``tarfa/engine/moe_kernel.py:129-139``).  torch's CPU and GPU
+streams differ and ~194 GB of full-size expert weights cannot be produced on the
+host, so weights, activations and router logits are instead a pure function of
+``(seed, stream, element index)``; the device twin of this file
+(``tarfa_amd/csrc/fill.hip``) produces bit-identical values, so the oracle can
+regenerate any single expert it needs.
+
+* hash  : splitmix64 output function (S. Vigna, "splitmix64.c", 2015, public
+          domain): ``h_i = mix(key + (i + 1) * 0x9E3779B97F4A7C15)``.
+* normal: Irwin-Hall sum of four uniforms, centred and scaled to unit variance.
+  - ``n16``: four 16-bit fields of one hash; the integer sum is exact, converted
+    to fp32 exactly and multiplied once by an fp32 constant (one IEEE rounding),
+    then rounded to bf16.  Used for bf16 weights and activations.
+  - ``n32``: four 32-bit fields of two hashes, summed exactly in int64, scaled in
+    fp64 and rounded once to fp32.  Used for fp32 router logits, where the
+    finer grid keeps exact ties out of the top-9.
+  The distribution is bounded at +-3.46 sigma (Irwin-Hall n=4); it stands in for
+  the reference's ``~N(0, sigma)``.
+"""
+import math
+
+import numpy as np
+
+from . import bf16
+
+GOLDEN = 0x9E3779B97F4A7C15
+M64 = (1 << 64) - 1
+STD16 = math.sqrt((65536.0 ** 2 - 1.0) / 3.0)   # std of a sum of four U{0..65535}
+STD32 = math.sqrt((2.0 ** 64 - 1.0) / 3.0)      # std of a sum of four U{0..2^32-1}
+
+# tensor kinds in a stream id: (layer << 40) | (kind << 32) | expert
+KIND_GATE_UP, KIND_DOWN, KIND_ROUTER, KIND_SH_GATE, KIND_SH_UP, KIND_SH_DOWN, \
+    KIND_SH_GATEW, KIND_X, KIND_LOGITS = range(9)
+
+
+def _mix_int(z):
+    z &= M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+    return z ^ (z >> 31)
+
+
+def stream_id(kind, layer=0, expert=0):
+    return (int(layer) << 40) | (int(kind) << 32) | int(expert)
+
+
+def key(seed, stream):
+    """Per-tensor key: mix(seed ^ mix(stream + GOLDEN))."""
+    return _mix_int((int(seed) & M64) ^ _mix_int(int(stream) + GOLDEN))
+
+
+def _mix(z):
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def hashes(k, start, n):
+    """h_i for i in [start, start + n) as uint64."""
+    with np.errstate(over="ignore"):
+        i = np.arange(start, start + n, dtype=np.uint64) + np.uint64(1)
+        return _mix(np.uint64(k) + i * np.uint64(GOLDEN))
+
+
+def scale16(std):
+    """fp32 multiplier applied to the centred 16-bit Irwin-Hall sum."""
+    return np.float32(std / STD16)
+
+
+def n16_f32(k, n, std, start=0):
+    h = hashes(k, start, n)
+    m = np.uint64(0xFFFF)
+    s = (h & m) + ((h >> np.uint64(16)) & m) + ((h >> np.uint64(32)) & m) + (h >> np.uint64(48))
+    c = s.astype(np.int64) - 131070
+    return c.astype(np.float32) * scale16(std)
+
+
+def n16_bf16_bits(k, n, std, start=0):
+    """bf16 bit patterns of ``n`` Irwin-Hall normals with standard deviation ``std``."""
+    return bf16.bits(n16_f32(k, n, std, start))
+
+
+def n32_f32(k, n, std, start=0):
+    """fp32 normals from two hashes per element (hash indices 2i and 2i+1)."""
+    h = hashes(k, 2 * start, 2 * n)
+    lo, hi = h[0::2], h[1::2]
+    m = np.uint64(0xFFFFFFFF)
+    s = ((lo & m).astype(np.int64) + (lo >> np.uint64(32)).astype(np.int64)
+         + (hi & m).astype(np.int64) + (hi >> np.uint64(32)).astype(np.int64))
+    c = s - 2 * 0xFFFFFFFF
+    return (c.astype(np.float64) * (std / STD32)).astype(np.float32)
+
+
+def tensor_bf16(seed, kind, shape, std, layer=0, expert=0):
+    """Seeded bf16 tensor (uint16 bit patterns) with row-major element indices."""
+    n = int(np.prod(shape))
+    return n16_bf16_bits(key(seed, stream_id(kind, layer, expert)), n, std).reshape(shape)
+
+
+def tensor_f32(seed, kind, shape, std, layer=0, expert=0):
+    n = int(np.prod(shape))
+    return n32_f32(key(seed, stream_id(kind, layer, expert)), n, std).reshape(shape)

@@ -1,0 +1,75 @@
+"""Loader for libtmoe.so (the HIP C-ABI library).
+
+``torch`` is imported first: libtmoe's HIP runtime symbols then resolve to the
+runtime torch has already mapped, so a process never holds two HIP runtimes
+(checked after loading).  A missing library raises -- there is no fallback path.
+"""
+import ctypes
+import os
+import re
+
+import torch  # noqa: F401  (must precede the library load, see module docstring)
+
+ABI_VERSION = 1
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtmoe.so")
+
+_c = ctypes
+_vp, _i, _u64, _sz, _f, _d = _c.c_void_p, _c.c_int, _c.c_uint64, _c.c_size_t, _c.c_float, _c.c_double
+
+# name -> (restype, argtypes); mirrors include/tmoe.h
+SIGNATURES = {
+    "tmoe_abi_version": (_i, []),
+    "tmoe_strerror": (_c.c_char_p, [_i]),
+    "tmoe_workspace_bytes": (_sz, [_i] * 6),
+    "tmoe_workspace_status": (_i, [_vp, _vp]),
+    "tmoe_fill_bf16": (_i, [_vp, _u64, _u64, _f, _u64, _vp]),
+    "tmoe_fill_f32": (_i, [_vp, _u64, _u64, _d, _u64, _vp]),
+    "tmoe_router_topk": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "tmoe_dispatch": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tmoe_experts_forward_bf16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "tmoe_moe_block_bf16": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                 _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+}
+
+_LIB = None
+
+
+def _hip_runtimes_mapped():
+    try:
+        with open("/proc/self/maps") as f:
+            maps = f.read()
+    except OSError:
+        return set()
+    return set(re.findall(r"\S*libamdhip64\.so\S*", maps))
+
+
+def lib():
+    """The loaded library (loaded on first use)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run `python -m tarfa_amd.build` (no CPU fallback exists)")
+    handle = _c.CDLL(LIB_PATH)
+    runtimes = _hip_runtimes_mapped()
+    if len(runtimes) > 1:
+        raise RuntimeError(f"two HIP runtimes mapped in one process: {sorted(runtimes)}")
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype, fn.argtypes = res, args
+    v = handle.tmoe_abi_version()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"libtmoe ABI {v}, expected {ABI_VERSION}: rebuild with `python -m tarfa_amd.build`")
+    _LIB = handle
+    return handle
+
+
+def check(status, what):
+    """Raise RuntimeError for a non-zero tmoe status."""
+    if status != 0:
+        msg = lib().tmoe_strerror(status).decode()
+        raise RuntimeError(f"{what}: tmoe status {status} ({msg})")
+
+
+def exported_symbols():
+    return sorted(SIGNATURES)

@@ -1,0 +1,148 @@
+// extern "C" entry points: argument validation, workspace carving, launches.
+#include "tmoe_device.h"
+#include "tmoe_ws.h"
+#include "tmoe_decode.h"
+
+namespace tmoe {
+int decode_launch(DecodeParams& p, bool run_router, hipStream_t s);
+int launch_router_logits(const uint16_t* x, const uint16_t* wg, int T, int H, int E, float* logits, hipStream_t s);
+int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64, uint16_t* wb, int32_t* ids32,
+                       float* wf, uint32_t* heat, hipStream_t s);
+int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
+                   const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
+                   const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
+                   void* ws, hipStream_t s);
+int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
+}  // namespace tmoe
+
+
+using namespace tmoe;
+
+static bool misaligned(const void* p) { return ((uintptr_t)p & 15u) != 0; }
+
+static int check_shape(int T, int H, int E, int I, int k, int Is) {
+  if (T < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E) return TMOE_ERR_SHAPE;
+  if (H < 8 || H > 4096 || H % 8) return TMOE_ERR_SHAPE;
+  if (I < 8 || I > 4096 || I % 8) return TMOE_ERR_SHAPE;
+  if (Is < 0 || Is > 4096 || Is % 8) return TMOE_ERR_SHAPE;
+  return TMOE_OK;
+}
+
+extern "C" int tmoe_abi_version(void) { return TMOE_ABI_VERSION; }
+
+extern "C" const char* tmoe_strerror(int status) {
+  switch (status) {
+    case TMOE_OK: return "ok";
+    case TMOE_ERR_NULL: return "a required pointer is NULL";
+    case TMOE_ERR_SHAPE: return "unsupported or inconsistent sizes";
+    case TMOE_ERR_ALIGN: return "a pointer is not 16-byte aligned";
+    case TMOE_ERR_WORKSPACE: return "workspace smaller than tmoe_workspace_bytes()";
+    case TMOE_ERR_HIP: return "HIP runtime call or kernel launch failed";
+    case TMOE_ERR_EXPERT_ID: return "expert id outside [0, num_experts] seen on the device";
+    default: return "unknown tmoe status";
+  }
+}
+
+extern "C" size_t tmoe_workspace_bytes(int T, int H, int E, int I, int k, int Is) {
+  if (check_shape(T, H, E, I, k, Is)) return 0;
+  return ws_layout(T, H, E, I, k, Is).total;
+}
+
+extern "C" int tmoe_workspace_status(void* workspace, void* stream) {
+  if (!workspace) return TMOE_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t flags = 0;
+  if (hipMemcpyAsync(&flags, workspace, sizeof(flags), hipMemcpyDeviceToHost, s) != hipSuccess) return TMOE_ERR_HIP;
+  if (hipStreamSynchronize(s) != hipSuccess) return TMOE_ERR_HIP;
+  if (!flags) return TMOE_OK;
+  const uint32_t zero = 0;
+  if (hipMemcpy(workspace, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess) return TMOE_ERR_HIP;
+  return TMOE_ERR_EXPERT_ID;
+}
+
+static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
+  p.status = ws_ptr<uint32_t>(ws, L.status);
+  p.logits_ws = ws_ptr<float>(ws, L.logits);
+  p.ids_ws = ws_ptr<int32_t>(ws, L.ids);
+  p.w_ws = ws_ptr<float>(ws, L.wts);
+  p.gs_ws = ws_ptr<float>(ws, L.gs);
+  p.act_ws = ws_ptr<uint16_t>(ws, L.act);
+  p.sact_ws = ws_ptr<uint16_t>(ws, L.act) + (size_t)p.k * p.I;
+  p.sh_ws = ws_ptr<uint16_t>(ws, L.sh);
+}
+
+extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
+                                         const uint64_t* expert_table, int H, int E, int I, int k, void* out,
+                                         void* workspace, size_t ws_bytes, void* stream) {
+  if (int st = check_shape(T, H, E, I, k, 0)) return st;
+  if (!x || !ids || !weights || !expert_table || !out || !workspace) return TMOE_ERR_NULL;
+  if (misaligned(x) || misaligned(workspace)) return TMOE_ERR_ALIGN;
+  const Ws L = ws_layout(T, H, E, I, k, 0);
+  if (ws_bytes < L.total) return TMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  if (T == 1) {
+    DecodeParams p{};
+    p.x = (const uint16_t*)x;
+    p.table = expert_table;
+    p.ids_in = ids;
+    p.w_in = (const uint16_t*)weights;
+    p.H = H; p.E = E; p.I = I; p.k = k; p.Is = 0;
+    p.out = (uint16_t*)out;
+    bind_ws(p, workspace, L);
+    return decode_launch(p, false, s);
+  }
+  return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
+                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s);
+}
+
+extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,
+                                   const uint64_t* expert_table, const void* sh_gate, const void* sh_up,
+                                   const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k, int Is,
+                                   void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  const bool has_sh = sh_gate || sh_up || sh_down || sh_gate_w;
+  if (has_sh && (!sh_gate || !sh_up || !sh_down || !sh_gate_w || Is < 8)) return TMOE_ERR_NULL;
+  if (!has_sh) Is = 0;
+  if (int st = check_shape(T, H, E, I, k, Is)) return st;
+  if (!x || !expert_table || !out || !workspace || (!router_w && !logits_in)) return TMOE_ERR_NULL;
+  if (misaligned(x) || misaligned(workspace) || (router_w && misaligned(router_w)) ||
+      (has_sh && (misaligned(sh_gate) || misaligned(sh_up) || misaligned(sh_down) || misaligned(sh_gate_w))))
+    return TMOE_ERR_ALIGN;
+  const Ws L = ws_layout(T, H, E, I, k, Is);
+  if (ws_bytes < L.total) return TMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  if (T == 1) {
+    DecodeParams p{};
+    p.x = (const uint16_t*)x;
+    p.router_w = logits_in ? nullptr : (const uint16_t*)router_w;
+    p.logits_in = logits_in;
+    p.table = expert_table;
+    p.sh_gate = (const uint16_t*)sh_gate;
+    p.sh_up = (const uint16_t*)sh_up;
+    p.sh_down = (const uint16_t*)sh_down;
+    p.sh_gate_w = (const uint16_t*)sh_gate_w;
+    p.H = H; p.E = E; p.I = I; p.k = k; p.Is = Is;
+    p.out = (uint16_t*)out;
+    p.ids_out = ids_out;
+    p.w_out = (uint16_t*)weights_out;
+    p.heat = heat;
+    bind_ws(p, workspace, L);
+    return decode_launch(p, true, s);
+  }
+  // T > 1: router, shared gate, then the prefill experts path with the shared expert as an extra group.
+  float* logits = ws_ptr<float>(workspace, L.logits);
+  int32_t* ids32 = ws_ptr<int32_t>(workspace, L.ids);
+  float* wf = ws_ptr<float>(workspace, L.wts);
+  float* gs = ws_ptr<float>(workspace, L.gs);
+  const float* lg = logits_in;
+  if (!lg) {
+    if (int st = launch_router_logits((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, logits, s)) return st;
+    lg = logits;
+  }
+  if (int st = launch_router_topk(lg, T, E, k, ids_out, (uint16_t*)weights_out, ids32, wf, heat, s)) return st;
+  if (has_sh)
+    if (int st = launch_shared_gate((const uint16_t*)x, (const uint16_t*)sh_gate_w, T, H, gs, s)) return st;
+  return prefill_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
+                        (const uint16_t*)sh_up, (const uint16_t*)sh_down, has_sh ? gs : nullptr, H, E, I, k, Is,
+                        (uint16_t*)out, workspace, s);
+}

@@ -1,0 +1,102 @@
+// Router for T tokens: fp32 logits GEMV (when logits are not supplied) and a
+// one-wave-per-token softmax / top-k / renormalise.
+//   transformers/.../modeling_qwen3_5_moe.py:768-776 (Qwen3_5MoeTopKRouter.forward),
+//   with fp32 logits in place of the hidden-dtype F.linear at :770.
+#include "tmoe_gemv.h"
+#include "tmoe_ws.h"
+
+namespace tmoe {
+
+// logits[t, e] = sum_h x[t, h] * wg[e, h] in fp32.  One block per token; wave w
+// handles experts w, w + 4, ...  (4 rows in flight per wave).
+template <int MAXC>
+__global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ wg, int H, int E,
+                                                       float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int t = blockIdx.x;
+  XFrag<MAXC> xf;
+  load_xfrag<MAXC>(xf, x + (size_t)t * H, H, lane);
+  for (int e0 = wid * 4; e0 < E; e0 += 16) {
+    const uint16_t* rows[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rows[r] = wg + (size_t)min(e0 + r, E - 1) * H;
+    float d[4];
+    wave_dots<MAXC, 4>(rows, xf, H, lane, d);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (e0 + r < E) logits[(size_t)t * E + e0 + r] = d[r];
+    }
+  }
+}
+
+// One wave per token.
+template <int MAXEPL>
+__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int T, int E, int k,
+                                                     int64_t* ids64, uint16_t* wb, int32_t* ids32, float* wf,
+                                                     uint32_t* heat) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  TopkOut o;
+  o.ids32 = ids32 ? ids32 + (size_t)t * k : nullptr;
+  o.wf = wf ? wf + (size_t)t * k : nullptr;
+  o.ids64 = ids64 ? ids64 + (size_t)t * k : nullptr;
+  o.wb = wb ? wb + (size_t)t * k : nullptr;
+  o.heat = heat;
+  wave_topk<MAXEPL>(logits + (size_t)t * E, false, E, k, lane, o);
+}
+
+int launch_router_logits(const uint16_t* x, const uint16_t* wg, int T, int H, int E, float* logits,
+                         hipStream_t s) {
+  const int nc = (H + 511) / 512;
+  switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
+    case 2: hipLaunchKernelGGL(k_router_logits<2>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
+    case 4: hipLaunchKernelGGL(k_router_logits<4>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
+    case 6: hipLaunchKernelGGL(k_router_logits<6>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
+    default: hipLaunchKernelGGL(k_router_logits<8>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
+  }
+  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+}
+
+int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64, uint16_t* wb, int32_t* ids32,
+                       float* wf, uint32_t* heat, hipStream_t s) {
+  const dim3 grid((T + 3) / 4), block(256);
+  const int epl = (E + 63) / 64;
+  if (epl <= 4)
+    hipLaunchKernelGGL(k_router_topk<4>, grid, block, 0, s, logits, T, E, k, ids64, wb, ids32, wf, heat);
+  else
+    hipLaunchKernelGGL(k_router_topk<16>, grid, block, 0, s, logits, T, E, k, ids64, wb, ids32, wf, heat);
+  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+}
+
+int check_router_shape(int T, int H, int E, int k) {
+  if (T < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E) return TMOE_ERR_SHAPE;
+  if (H < 8 || H > 4096 || H % 8) return TMOE_ERR_SHAPE;
+  return TMOE_OK;
+}
+
+}  // namespace tmoe
+
+extern "C" int tmoe_router_topk(const void* x, const void* router_w, const float* logits_in, int T, int H, int E,
+                                int k, int64_t* ids_out, void* weights_out, float* logits_out, uint32_t* heat,
+                                void* stream) {
+  using namespace tmoe;
+  if (int st = check_router_shape(T, H, E, k)) return st;
+  if (!ids_out || !weights_out) return TMOE_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  const float* lg = logits_in;
+  if (!lg) {
+    if (!x || !router_w || !logits_out) return TMOE_ERR_NULL;   // logits need a home when computed
+    if (((uintptr_t)x | (uintptr_t)router_w) & 15) return TMOE_ERR_ALIGN;
+    if (int st = launch_router_logits((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, logits_out, s))
+      return st;
+    lg = logits_out;
+  } else if (logits_out && logits_out != logits_in) {
+    if (hipMemcpyAsync(logits_out, logits_in, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, s) !=
+        hipSuccess)
+      return TMOE_ERR_HIP;
+  }
+  return launch_router_topk(lg, T, E, k, ids_out, (uint16_t*)weights_out, nullptr, nullptr, heat, s);
+}

@@ -1,0 +1,37 @@
+// Parameter block of the batch-1 (decode) kernels, shared with the ABI layer.
+#pragma once
+
+#include <stdint.h>
+
+namespace tmoe {
+
+struct DecodeParams {
+  const uint16_t* x;          // [H]
+  const uint16_t* router_w;   // [E, H] or null (logits supplied or experts-only mode)
+  const float* logits_in;     // [E] or null
+  const uint64_t* table;      // [E][2] gate_up / down base pointers
+  const uint16_t* sh_gate;    // [Is, H]   (null = no shared expert)
+  const uint16_t* sh_up;      // [Is, H]
+  const uint16_t* sh_down;    // [H, Is]
+  const uint16_t* sh_gate_w;  // [H]
+  const int64_t* ids_in;      // [k] experts-only mode (router skipped), else null
+  const uint16_t* w_in;       // [k] bf16
+  int H, E, I, k, Is;
+  int n_router_blocks, n_shared_up_blocks;
+  int n_up_blocks_per_expert, n_shared_down_blocks;
+  uint16_t* out;              // [H]
+  int64_t* ids_out;           // optional
+  uint16_t* w_out;            // optional
+  float* logits_out;          // optional
+  uint32_t* heat;             // optional
+  uint32_t* status;           // workspace
+  float* logits_ws;           // [E + 1]
+  int32_t* ids_ws;            // [k]
+  float* w_ws;                // [k]
+  float* gs_ws;               // [1]
+  uint16_t* act_ws;           // [k * I]
+  uint16_t* sact_ws;          // [Is]
+  uint16_t* sh_ws;            // [H]
+};
+
+}  // namespace tmoe

@@ -1,0 +1,120 @@
+// Device-side helpers shared by the tmoe kernels (gfx950, wave64).
+//
+// bf16 values travel as raw 16-bit patterns; conversions are explicit bit
+// operations so the rounding is round-to-nearest-even exactly as torch's
+// .to(torch.bfloat16) rounds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tmoe.h"
+
+namespace tmoe {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+// Round an fp32 value to the nearest bf16 value, kept in fp32.
+__device__ __forceinline__ float rbf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// 16-byte global loads.  Weight streams are read exactly once per call, so they
+// carry the non-temporal hint; small shared vectors (x, activations) do not.
+__device__ __forceinline__ u32x4 ld_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Dot of 8 bf16 weights (packed in 4 dwords) with 8 fp32 activations.
+__device__ __forceinline__ float dot8(const u32x4 w, const float* x, float acc) {
+  acc = fmaf(bf16_lo(w.x), x[0], acc);
+  acc = fmaf(bf16_hi(w.x), x[1], acc);
+  acc = fmaf(bf16_lo(w.y), x[2], acc);
+  acc = fmaf(bf16_hi(w.y), x[3], acc);
+  acc = fmaf(bf16_lo(w.z), x[4], acc);
+  acc = fmaf(bf16_hi(w.z), x[5], acc);
+  acc = fmaf(bf16_lo(w.w), x[6], acc);
+  acc = fmaf(bf16_hi(w.w), x[7], acc);
+  return acc;
+}
+// Same with both operands packed bf16.
+__device__ __forceinline__ float dot8bb(const u32x4 w, const u32x4 a, float acc) {
+  acc = fmaf(bf16_lo(w.x), bf16_lo(a.x), acc);
+  acc = fmaf(bf16_hi(w.x), bf16_hi(a.x), acc);
+  acc = fmaf(bf16_lo(w.y), bf16_lo(a.y), acc);
+  acc = fmaf(bf16_hi(w.y), bf16_hi(a.y), acc);
+  acc = fmaf(bf16_lo(w.z), bf16_lo(a.z), acc);
+  acc = fmaf(bf16_hi(w.z), bf16_hi(a.z), acc);
+  acc = fmaf(bf16_lo(w.w), bf16_lo(a.w), acc);
+  acc = fmaf(bf16_hi(w.w), bf16_hi(a.w), acc);
+  return acc;
+}
+
+// DPP lane moves (gfx9 encodings): quad_perm xor1 / xor2, row_half_mirror, row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// Sum over the 64 lanes of a wave in a fixed order; every lane gets the result.
+// Lanes are first summed within each row of 16 (quad xor 1, xor 2, half-row
+// mirror, row mirror), then the four row sums are added in row order.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+__device__ __forceinline__ int wave_min_int(int v) {
+  v = min(v, __builtin_amdgcn_mov_dpp(v, kDppXor1, 0xF, 0xF, true) );
+  v = min(v, __builtin_amdgcn_mov_dpp(v, kDppXor2, 0xF, 0xF, true));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, kDppHalfMirror, 0xF, 0xF, true));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, kDppMirror, 0xF, 0xF, true));
+  int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return min(min(a, b), min(c, d));
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+__device__ __forceinline__ float sigmoid_f32(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// SwiGLU activation at the reference's bf16 rounding points:
+// bf16(bf16(silu(g)) * u) with g, u already bf16 values.
+__device__ __forceinline__ float swiglu_bf16(float g, float u) { return rbf16(rbf16(silu_f32(g)) * u); }
+
+}  // namespace tmoe

@@ -1,0 +1,126 @@
+// Wave-level building blocks for the batch-1 (decode) path: bf16 row GEMVs with
+// fp32 accumulation streamed as 16-byte loads, and the single-wave top-k.
+#pragma once
+
+#include <math.h>
+
+#include "tmoe_device.h"
+
+namespace tmoe {
+
+// A vector of K bf16 values as seen by one wave: lane l holds columns
+// c*512 + 8l .. +7 of chunk c (c < nc = ceil(K/512)), converted to fp32.
+// Columns at or past K read as zero, so rows of any K % 8 == 0 work.
+template <int MAXC>
+struct XFrag {
+  float v[MAXC][8];
+};
+
+template <int MAXC>
+__device__ __forceinline__ void load_xfrag(XFrag<MAXC>& f, const uint16_t* __restrict__ x, int K, int lane) {
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int col = c * 512 + lane * 8;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (col < K) w = ld16(x + col);
+    f.v[c][0] = bf16_lo(w.x); f.v[c][1] = bf16_hi(w.x);
+    f.v[c][2] = bf16_lo(w.y); f.v[c][3] = bf16_hi(w.y);
+    f.v[c][4] = bf16_lo(w.z); f.v[c][5] = bf16_hi(w.z);
+    f.v[c][6] = bf16_lo(w.w); f.v[c][7] = bf16_hi(w.w);
+  }
+}
+
+// Dots of R weight rows (each K contiguous bf16) with the fragment; all R x nc
+// 16-byte loads are issued before any arithmetic.  Every lane gets the sums.
+template <int MAXC, int R>
+__device__ __forceinline__ void wave_dots(const uint16_t* const (&rows)[R], const XFrag<MAXC>& xf, int K, int lane,
+                                          float (&out)[R]) {
+  u32x4 w[R][MAXC];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int col = c * 512 + lane * 8;
+      w[r][c] = (col < K) ? ld_stream(rows[r] + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) acc = dot8(w[r][c], xf.v[c], acc);
+    out[r] = wave_sum(acc);
+  }
+}
+
+// Top-k of E fp32 logits by one wave (lane l owns experts l + 64 i, i < MAXEPL).
+// Order: logit descending, ties to the lower expert index.  Probabilities are
+// softmax in fp32 (max-subtracted), renormalised over the k selected in router
+// order, then rounded to bf16 -- transformers/.../modeling_qwen3_5_moe.py:771-774.
+struct TopkOut {
+  int32_t* ids32;    // [k] or null
+  float* wf;         // [k] bf16 values as fp32, or null
+  int64_t* ids64;    // [k] or null
+  uint16_t* wb;      // [k] bf16 or null
+  uint32_t* heat;    // [E] or null
+};
+
+template <int MAXEPL>
+__device__ __forceinline__ void wave_topk(const float* src, bool coherent, int E, int k, int lane, const TopkOut& o) {
+  float v[MAXEPL];
+#pragma unroll
+  for (int i = 0; i < MAXEPL; ++i) {
+    const int e = lane + 64 * i;
+    float val = -INFINITY;
+    if (e < E) val = coherent ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : src[e];
+    v[i] = val;
+  }
+  float lm = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MAXEPL; ++i) lm = fmaxf(lm, v[i]);
+  const float m = wave_max(lm);
+  float ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXEPL; ++i)
+    if (lane + 64 * i < E) ls += expf(v[i] - m);
+  const float S = wave_sum(ls);
+
+  uint32_t sel = 0;
+  float p[16];
+  int id[16];
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    id[r] = INT_MAX;
+    p[r] = 0.f;
+    if (r >= k) continue;                         // k is wave-uniform
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < MAXEPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !((sel >> i) & 1u) && (bi == INT_MAX || v[i] > bv)) { bv = v[i]; bi = e; }
+    }
+    const float g = wave_max(bv);
+    const int win = wave_min_int((bi != INT_MAX && bv == g) ? bi : INT_MAX);
+    if (win != INT_MAX && (win & 63) == lane) sel |= 1u << (win >> 6);
+    id[r] = win;
+    p[r] = (win == INT_MAX) ? 0.f : expf(g - m) / S;
+    psum += p[r];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (r >= k) continue;
+      const bool ok = id[r] != INT_MAX;
+      const int e = ok ? id[r] : E;                 // unselectable -> the skip sentinel E
+      const uint16_t wb = ok ? f32_to_bf16(p[r] / psum) : (uint16_t)0;
+      if (o.ids32) o.ids32[r] = e;
+      if (o.wf) o.wf[r] = bf16_to_f32(wb);
+      if (o.ids64) o.ids64[r] = e;
+      if (o.wb) o.wb[r] = wb;
+      if (o.heat && ok) atomicAdd(o.heat + e, 1u);
+    }
+  }
+}
+
+}  // namespace tmoe

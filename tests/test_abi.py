@@ -1,0 +1,57 @@
+"""The C ABI library loads and exports every entry point include/tmoe.h declares (no GPU calls)."""
+import ctypes
+import os
+import re
+
+from tarfa_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "tmoe.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tmoe_\w+)\s*\(", text)))
+
+
+def test_header_declares_what_the_loader_binds():
+    assert declared() == _lib.exported_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(handle, n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_strerror():
+    lib = _lib.lib()
+    assert lib.tmoe_abi_version() == _lib.ABI_VERSION
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.tmoe_strerror(code).decode() != "unknown tmoe status"
+    assert lib.tmoe_strerror(-99).decode() == "unknown tmoe status"
+
+
+def test_workspace_sizes_and_shape_validation():
+    lib = _lib.lib()
+    n1 = lib.tmoe_workspace_bytes(1, 2560, 256, 1024, 8, 1024)
+    n4k = lib.tmoe_workspace_bytes(4096, 2560, 256, 1024, 8, 1024)
+    assert 0 < n1 < n4k
+    assert n4k >= 4096 * 8 * 2560 * 2            # per-assignment expert outputs for the combine
+    assert lib.tmoe_workspace_bytes(1, 2561, 256, 1024, 8, 0) == 0      # H % 8
+    assert lib.tmoe_workspace_bytes(1, 2560, 256, 1024, 9, 0) > 0
+    assert lib.tmoe_workspace_bytes(1, 2560, 4, 1024, 8, 0) == 0        # k > E
+    assert lib.tmoe_workspace_bytes(0, 2560, 256, 1024, 8, 0) == 0
+
+
+def test_entry_points_reject_bad_arguments_without_touching_the_device():
+    lib = _lib.lib()
+    # NULL pointers and bad shapes are rejected on the host before any launch
+    assert lib.tmoe_experts_forward_bf16(None, 1, None, None, None, 2560, 256, 1024, 8, None, None, 0, None) == -1
+    assert lib.tmoe_experts_forward_bf16(None, 1, None, None, None, 2561, 256, 1024, 8, None, None, 0, None) == -2
+    assert lib.tmoe_moe_block_bf16(None, 1, None, None, None, None, None, None, None, 2560, 256, 1024, 8, 0,
+                                   None, None, None, None, None, 0, None) == -1
+    assert lib.tmoe_router_topk(None, None, None, 1, 2560, 256, 8, None, None, None, None, None) == -1
+    assert lib.tmoe_router_topk(None, None, None, 1, 2560, 256, 17, None, None, None, None, None) == -2
+    assert lib.tmoe_dispatch(None, 4, 8, 256, None, None, None, None, 0, None) == -1
+    assert lib.tmoe_fill_bf16(None, 16, 1, 1.0, 0, None) == -1

@@ -1,0 +1,181 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: bit-exact for the generator, top-k ids and the dispatch permutation;
+bf16 layer outputs within max-abs 2e-2 and rel-L2 1e-3 (accumulation order:
+bf16 rounding after each GEMV, SiLU, multiply, weight-scale and add; decode in
+router order, prefill in ascending expert id).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16, moe, rng
+from tarfa_amd import seeded
+from tarfa_amd import moe as tm
+from tarfa_amd.moe import MoEShape, Workspace
+from tests._util import assert_close_bf16, expert_dicts, f32
+
+pytestmark = pytest.mark.gpu
+
+SMALL = MoEShape(1024, 32, 512, 8, 0)            # the reference-CPU-sized layer
+FULL = MoEShape(2560, 256, 1024, 8, 1024)        # full-size layer with a shared expert
+
+
+def bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_fill_matches_oracle_generator(gpu):
+    for n, start in ((1003, 0), (4096, 77), (8, 1 << 33)):
+        k = rng.key(11, rng.stream_id(rng.KIND_GATE_UP, 2, 5))
+        t = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+        tm.fill_bf16(t, k, 0.02, start=start)
+        assert np.array_equal(bits(t), rng.n16_bf16_bits(k, n, 0.02, start=start))
+        f = torch.empty(n, dtype=torch.float32, device=gpu)
+        tm.fill_f32(f, k, 1.0, start=start)
+        assert np.array_equal(f.cpu().numpy(), rng.n32_f32(k, n, 1.0, start=start))
+    layer = seeded.make_layer(SMALL, seed=3, layer=1, device=gpu)
+    for e in (0, 17, 31):
+        want = rng.tensor_bf16(3, rng.KIND_GATE_UP, (1024, 1024), 0.02, 1, e)
+        assert np.array_equal(bits(layer.gate_up[e]), want)
+        want = rng.tensor_bf16(3, rng.KIND_DOWN, (1024, 512), 0.02, 1, e)
+        assert np.array_equal(bits(layer.down[e]), want)
+    assert np.array_equal(bits(layer.router_w), rng.tensor_bf16(3, rng.KIND_ROUTER, (32, 1024), 0.02, 1))
+
+
+def _check_routing(ids, w, logits_ref, k, what):
+    """Top-k ids equal wherever the oracle's top-(k+1) gap exceeds fp32 dot-order noise."""
+    ids_ref, w_ref, _ = moe.router_topk(logits_ref, k)
+    gaps = moe.topk_gaps(logits_ref, k)
+    clear = gaps > 1e-5 * np.maximum(1.0, np.abs(logits_ref).max(axis=-1))
+    assert clear.mean() > 0.95, f"{what}: too many near-ties ({(~clear).sum()})"
+    assert np.array_equal(ids[clear], ids_ref[clear]), f"{what}: top-k ids differ"
+    wd = np.abs(w[clear] - w_ref[clear])
+    assert np.all(wd <= np.abs(w_ref[clear]) * 2.0 ** -7), f"{what}: routing weights beyond one bf16 ulp"
+    return ids_ref, w_ref
+
+
+@pytest.mark.parametrize("H,E,k,T", [(1024, 32, 8, 64), (2560, 256, 8, 64), (512, 64, 4, 7)])
+def test_router_topk_multi_token(gpu, H, E, k, T):
+    shape = MoEShape(H, E, 256, k)
+    wg = seeded.make_layer(MoEShape(H, E, 8, k), seed=5, device=gpu).router_w
+    x = seeded.make_tokens(shape, 5, T, device=gpu)
+    ids, w, logits = tm.router_topk(shape, x=x, router_w=wg)
+    lg_ref = moe.router_logits(f32(x), f32(wg))
+    np.testing.assert_allclose(logits.cpu().numpy(), lg_ref, rtol=1e-5, atol=1e-5)
+    _check_routing(ids.cpu().numpy(), f32(w), lg_ref, k, "router")
+    # supplied logits: selection on identical fp32 inputs is bit-exact
+    ids2, w2, _ = tm.router_topk(shape, logits=torch.from_numpy(lg_ref).to(gpu))
+    ids_ref, w_ref, _ = moe.router_topk(lg_ref, k)
+    assert np.array_equal(ids2.cpu().numpy(), ids_ref)
+    assert np.all(np.abs(f32(w2) - w_ref) <= np.abs(w_ref) * 2.0 ** -7)
+
+
+def _decode_case(shape, seed, gpu, layer=None):
+    layer = layer or seeded.make_layer(shape, seed, device=gpu)
+    ws = Workspace(shape, gpu)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    x = seeded.make_tokens(shape, seed, 1, device=gpu)
+    out, ids, w = tm.moe_block(shape, x, table, ws, router_w=layer.router_w, shared=layer.shared)
+    torch.cuda.synchronize()
+    xs = f32(x)
+    lg = moe.router_logits(xs, f32(layer.router_w))
+    ids_ref, w_ref = _check_routing(ids.cpu().numpy(), f32(w), lg, shape.top_k, "decode router")
+    gu, dn = expert_dicts(layer.gate_up, layer.down, ids_ref)
+    ref = moe.experts_decode(xs[0], ids_ref[0], w_ref[0], gu, dn, shape.num_experts)
+    if layer.shared is not None:
+        ref = moe.add_bf16(ref, moe.shared_expert(xs[0], *[f32(t) for t in layer.shared]))
+    assert_close_bf16(f32(out)[0], ref, f"decode block seed {seed}")
+    # experts.forward boundary with the oracle's routing
+    out2 = tm.experts_forward(shape, x, torch.from_numpy(ids_ref).to(gpu),
+                              torch.from_numpy(w_ref).to(gpu, torch.bfloat16), table, ws)
+    ref2 = moe.experts_decode(xs[0], ids_ref[0], w_ref[0], gu, dn, shape.num_experts)
+    assert_close_bf16(f32(out2)[0], ref2, f"decode experts seed {seed}")
+    ws.status()
+    return layer
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_decode_small_layer(gpu, seed):
+    _decode_case(SMALL, seed, gpu)
+
+
+def test_decode_full_size_layer(gpu):
+    layer = _decode_case(FULL, 100, gpu)
+    _decode_case(FULL, 101, gpu, layer=None)
+    del layer
+
+
+def test_decode_sentinel_and_invalid_ids(gpu):
+    shape = MoEShape(512, 16, 256, 4)
+    layer = seeded.make_layer(shape, 9, device=gpu)
+    ws = Workspace(shape, gpu)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    x = seeded.make_tokens(shape, 9, 1, device=gpu)
+    ids = torch.tensor([[3, 16, 7, 1]], device=gpu)             # 16 = the skip sentinel E
+    w = torch.tensor([[0.4, 0.3, 0.2, 0.1]], device=gpu).to(torch.bfloat16)
+    out = tm.experts_forward(shape, x, ids, w, table, ws)
+    gu, dn = expert_dicts(layer.gate_up, layer.down, ids.cpu().numpy())
+    ref = moe.experts_decode(f32(x)[0], ids.cpu().numpy()[0], f32(w)[0], gu, dn, 16)
+    assert_close_bf16(f32(out)[0], ref, "sentinel")
+    ws.status()                                                  # the sentinel is not an error
+    bad = torch.tensor([[3, 99, 7, 1]], device=gpu)
+    tm.experts_forward(shape, x, bad, w, table, ws)
+    with pytest.raises(RuntimeError, match="expert id"):
+        ws.status()
+
+
+@pytest.mark.parametrize("T,E,k", [(4096, 256, 8), (5, 32, 8), (1000, 16, 1), (300, 4, 2)])
+def test_dispatch_bit_exact(gpu, T, E, k):
+    g = np.random.default_rng(T + E)
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    if T > 10:
+        ids[3, 0] = E                                            # sentinel rows are skipped
+    ws = Workspace(MoEShape(128, E, 64, k), gpu, tokens=T)
+    offsets, perm, inv = tm.dispatch(torch.from_numpy(ids).to(gpu), E, ws)
+    o_ref, p_ref = moe.dispatch(ids, E)
+    assert np.array_equal(offsets.cpu().numpy(), o_ref)
+    n = int(o_ref[-1])
+    assert np.array_equal(perm.cpu().numpy()[:n], p_ref)
+    inv_ref = np.full(T * k, -1, np.int64)
+    inv_ref[p_ref] = np.arange(n)
+    assert np.array_equal(inv.cpu().numpy(), inv_ref)
+
+
+@pytest.mark.parametrize("T,shared", [(2, False), (37, True), (300, True)])
+def test_prefill_small_block(gpu, T, shared):
+    shape = MoEShape(256, 16, 128, 4, 128 if shared else 0)
+    layer = seeded.make_layer(shape, 40 + T, device=gpu)
+    ws = Workspace(shape, gpu, tokens=T)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    x = seeded.make_tokens(shape, 40 + T, T, device=gpu)
+    logits = seeded.make_logits(shape, 40 + T, T, device=gpu)
+    out, ids, w = tm.moe_block(shape, x, table, ws, logits=logits, shared=layer.shared)
+    lg = logits.cpu().numpy()
+    ids_ref, w_ref, _ = moe.router_topk(lg, shape.top_k)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    xs = f32(x)
+    gu, dn = expert_dicts(layer.gate_up, layer.down, ids_ref)
+    ref = moe.experts_prefill(xs, ids_ref, f32(w), gu, dn, shape.num_experts)
+    if shared:
+        ref = moe.add_bf16(ref, moe.shared_expert(xs, *[f32(t) for t in layer.shared]))
+    assert_close_bf16(f32(out), ref, f"prefill T={T}")
+    out2 = tm.experts_forward(shape, x, ids, w, table, ws)
+    ref2 = moe.experts_prefill(xs, ids_ref, f32(w), gu, dn, shape.num_experts)
+    assert_close_bf16(f32(out2), ref2, f"prefill experts T={T}")
+
+
+def test_prefill_group_larger_than_one_tile(gpu):
+    """Skewed routing: one expert receives every token (> 256 rows -> several M-chunks)."""
+    shape = MoEShape(256, 8, 128, 2)
+    T = 600
+    layer = seeded.make_layer(shape, 77, device=gpu)
+    ws = Workspace(shape, gpu, tokens=T)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    x = seeded.make_tokens(shape, 77, T, device=gpu)
+    ids = torch.stack([torch.zeros(T, dtype=torch.int64), torch.arange(T) % 7 + 1], dim=1).to(gpu)
+    w = torch.full((T, 2), 0.5, device=gpu).to(torch.bfloat16)
+    out = tm.experts_forward(shape, x, ids, w, table, ws)
+    gu, dn = expert_dicts(layer.gate_up, layer.down, ids.cpu().numpy())
+    ref = moe.experts_prefill(f32(x), ids.cpu().numpy(), f32(w), gu, dn, 8)
+    assert_close_bf16(f32(out), ref, "skewed prefill")

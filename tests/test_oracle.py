@@ -1,0 +1,350 @@
+"""CPU pins of the oracle against independent implementations (no GPU).
+
+Each oracle function is checked against something other than its own formula:
+torch's bf16 cast and op chain, transformers' Qwen3.5-MoE modules (the
+third-party code the reference calls), brute-force one_hot/where, exhaustive
+enumeration, a published known-answer vector, or the reference's own
+known-answer criterion.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import bf16, int4, moe, rng
+from tests._util import rel_l2
+
+BF = torch.bfloat16
+
+
+def tb(a):
+    """numpy fp32 (bf16 values) -> torch bf16 (exact)."""
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(BF)
+
+
+# ------------------------------------------------------------------ bf16
+
+def test_bf16_rounding_matches_torch_random_patterns():
+    g = np.random.default_rng(0)
+    u = g.integers(0, 2 ** 32, 1 << 22, dtype=np.uint64).astype(np.uint32)
+    f = u.view(np.float32)
+    f = f[np.isfinite(f)]
+    want = torch.from_numpy(f).to(BF).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(bf16.bits(f), want)
+
+
+def test_bf16_rounding_ties_and_edges():
+    # exact ties (low half 0x8000) round to even; max finite rounds to inf like torch
+    hi = np.arange(0, 1 << 16, dtype=np.uint32)
+    f = ((hi << 16) | 0x8000).view(np.float32)
+    f = f[np.isfinite(f)]
+    want = torch.from_numpy(f).to(BF).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(bf16.bits(f), want)
+    edges = np.array([0.0, -0.0, 1e-45, -1e-45, 3.4028235e38, -3.4028235e38, np.inf, -np.inf], np.float32)
+    want = torch.from_numpy(edges).to(BF).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(bf16.bits(edges), want)
+    assert np.isnan(bf16.to_f32(bf16.bits(np.array([np.nan], np.float32))))[0]
+
+
+# ------------------------------------------------------------------ generator
+
+def test_splitmix64_known_answer():
+    # splitmix64.c (Vigna), state seeded with 1234567: first five outputs
+    assert [int(v) for v in rng.hashes(1234567, 0, 5)] == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423,
+        4593380528125082431, 16408922859458223821]
+
+
+def test_generator_vectorised_equals_bigint():
+    k = rng.key(42, rng.stream_id(rng.KIND_DOWN, 3, 17))
+    h = rng.hashes(k, 1000, 64)
+    for i in range(64):
+        assert int(h[i]) == rng._mix_int(k + (1000 + i + 1) * rng.GOLDEN)
+    # n16: the centred sum of four 16-bit fields, times one fp32 constant
+    z = rng.n16_f32(k, 64, 0.02, start=1000)
+    for i in range(64):
+        v = int(h[i])
+        c = sum((v >> s) & 0xFFFF for s in (0, 16, 32, 48)) - 131070
+        assert z[i] == np.float32(np.float32(c) * rng.scale16(0.02))
+
+
+def test_generator_moments_and_determinism():
+    k = rng.key(7, rng.stream_id(rng.KIND_GATE_UP, 0, 1))
+    a = rng.n16_f32(k, 1 << 20, 1.0)
+    assert abs(a.mean()) < 5e-3 and abs(a.std() - 1.0) < 5e-3
+    assert np.array_equal(a[1000:2000], rng.n16_f32(k, 1000, 1.0, start=1000))
+    b = rng.n32_f32(k, 1 << 18, 1.0)
+    assert abs(b.mean()) < 1e-2 and abs(b.std() - 1.0) < 1e-2
+    assert np.array_equal(b[500:600], rng.n32_f32(k, 100, 1.0, start=500))
+    # distinct streams are uncorrelated
+    c = rng.n16_f32(rng.key(7, rng.stream_id(rng.KIND_GATE_UP, 0, 2)), 1 << 20, 1.0)
+    assert abs(np.corrcoef(a, c)[0, 1]) < 5e-3
+
+
+# ------------------------------------------------------------------ router
+
+@pytest.mark.parametrize("E,k", [(32, 8), (256, 8), (64, 4)])
+def test_router_topk_matches_torch(E, k):
+    logits = rng.tensor_f32(3, rng.KIND_LOGITS, (512, E), 1.0)
+    assert np.min(moe.topk_gaps(logits, k)) > 0          # no ties: torch's order is defined
+    ids, w, probs = moe.router_topk(logits, k)
+    lt = torch.from_numpy(logits)
+    p = torch.softmax(lt, dim=-1, dtype=torch.float)
+    tv, ti = torch.topk(p, k, dim=-1)
+    tv = (tv / tv.sum(dim=-1, keepdim=True)).to(BF)
+    assert np.array_equal(ids, ti.numpy())
+    tw = tv.float().numpy()
+    assert np.mean(tw == w) > 0.99
+    assert np.all(np.abs(tw - w) <= np.abs(tw) * 2.0 ** -7)   # at most one bf16 ulp apart
+    assert np.allclose(probs, p.numpy(), rtol=1e-6, atol=1e-9)
+
+
+def test_router_logits_and_transformers_router_fp32():
+    from transformers.models.qwen3_5_moe import configuration_qwen3_5_moe as C, modeling_qwen3_5_moe as M
+    H, E, k = 256, 32, 8
+    cfg = C.Qwen3_5MoeTextConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k, moe_intermediate_size=64)
+    router = M.Qwen3_5MoeTopKRouter(cfg)
+    wg = bf16.to_f32(rng.tensor_bf16(5, rng.KIND_ROUTER, (E, H), 0.02))
+    x = bf16.to_f32(rng.tensor_bf16(5, rng.KIND_X, (64, H), 1.0))
+    with torch.no_grad():
+        router.weight.copy_(torch.from_numpy(wg))                  # fp32 module: fp32 logits
+        tl, tw, ti = router(torch.from_numpy(x))
+    lg = moe.router_logits(x, wg)
+    np.testing.assert_allclose(lg, tl.numpy(), rtol=1e-5, atol=1e-5)
+    assert np.min(moe.topk_gaps(lg, k)) > 1e-4
+    ids, w, _ = moe.router_topk(lg, k)
+    assert np.array_equal(ids, ti.numpy())
+    np.testing.assert_allclose(w, tw.numpy(), rtol=2.0 ** -8)
+
+
+def test_router_tie_breaks_to_lower_index():
+    lg = np.array([[0.5, 1.0, 1.0, 0.2, 1.0, 0.9]], np.float32)
+    ids, _, _ = moe.router_topk(lg, 3)
+    assert ids.tolist() == [[1, 2, 4]]
+
+
+# ------------------------------------------------------------------ dispatch
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 32), (2, 2, 4), (7, 3, 5), (33, 8, 32), (64, 1, 16)])
+def test_dispatch_matches_one_hot_where(T, k, E):
+    g = np.random.default_rng(T * 100 + k)
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    offsets, perm = moe.dispatch(ids, E)
+    mask = F.one_hot(torch.from_numpy(ids), num_classes=E).permute(2, 1, 0)      # fused_int4.py:228
+    hit = torch.greater(mask.sum(dim=(-1, -2)), 0).nonzero().flatten().tolist()   # :229
+    rows, counts = [], np.zeros(E, np.int64)
+    for e in hit:
+        pos, tok = torch.where(mask[e])                                            # :241
+        rows += (tok * k + pos).tolist()
+        counts[e] = len(tok)
+    assert perm.tolist() == rows
+    assert offsets.tolist() == [0] + np.cumsum(counts).tolist()
+
+
+def test_dispatch_drops_sentinel_and_out_of_range():
+    ids = np.array([[0, 4], [4, 1], [2, 9]], np.int64)       # E = 4: id 4 is the sentinel, 9 invalid
+    offsets, perm = moe.dispatch(ids, 4)
+    assert offsets.tolist() == [0, 1, 2, 3, 3]
+    assert perm.tolist() == [0, 3, 4]
+
+
+# ------------------------------------------------------------------ expert compute
+
+def _layer(seed, H, E, I, Is=0):
+    gu = {e: bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_GATE_UP, (2 * I, H), 0.02, 0, e)) for e in range(E)}
+    dn = {e: bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_DOWN, (H, I), 0.02, 0, e)) for e in range(E)}
+    wg = bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_ROUTER, (E, H), 0.02))
+    sh = None
+    if Is:
+        sh = (bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_SH_GATE, (Is, H), 0.02)),
+              bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_SH_UP, (Is, H), 0.02)),
+              bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_SH_DOWN, (H, Is), 0.02)),
+              bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_SH_GATEW, (H,), 0.02)))
+    return gu, dn, wg, sh
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_decode_matches_reference_op_chain(seed):
+    """The literal torch op sequence of fused_int4.py:180, 192-194 on CPU in bf16."""
+    H, E, I, k = 1024, 32, 512, 8
+    gu, dn, wg, _ = _layer(seed, H, E, I)
+    x = bf16.to_f32(rng.tensor_bf16(seed, rng.KIND_X, (1, H), 1.0))
+    ids, w, _ = moe.router_topk(moe.router_logits(x, wg), k)
+    got = moe.experts_decode(x[0], ids[0], w[0], gu, dn, E)
+    xt = tb(x[0])
+    acc = torch.zeros_like(xt)
+    rwl = tb(w[0])
+    for j, e in enumerate(ids[0].tolist()):
+        g, u = F.linear(xt, tb(gu[e])).chunk(2, dim=-1)
+        acc = acc + rwl[j] * F.linear(F.silu(g) * u, tb(dn[e]))
+    ref = acc.float().numpy()
+    assert rel_l2(got, ref) <= 1e-3 and np.max(np.abs(got - ref)) <= 2e-2
+    assert np.mean(got == ref) >= 0.95
+
+
+def test_decode_order_matters():
+    """Router order vs ascending-id order differ beyond the tolerance -- the pin is not vacuous."""
+    H, E, I, k = 1024, 32, 512, 8
+    gu, dn, wg, _ = _layer(11, H, E, I)
+    x = bf16.to_f32(rng.tensor_bf16(11, rng.KIND_X, (1, H), 1.0))
+    ids, w, _ = moe.router_topk(moe.router_logits(x, wg), k)
+    a = moe.experts_decode(x[0], ids[0], w[0], gu, dn, E)
+    o = np.argsort(ids[0])
+    b = moe.experts_decode(x[0], ids[0][o], w[0][o], gu, dn, E)
+    assert rel_l2(a, b) > 1e-3
+
+
+def _tf_block(H, E, I, k, Is):
+    from transformers.models.qwen3_5_moe import configuration_qwen3_5_moe as C, modeling_qwen3_5_moe as M
+    cfg = C.Qwen3_5MoeTextConfig(hidden_size=H, num_experts=E, moe_intermediate_size=I, num_experts_per_tok=k,
+                                 shared_expert_intermediate_size=Is, hidden_act="silu")
+    return M.Qwen3_5MoeSparseMoeBlock(cfg).to(BF)
+
+
+def _load_tf_block(blk, gu, dn, wg, sh):
+    E = len(gu)
+    with torch.no_grad():
+        blk.experts.gate_up_proj.copy_(torch.stack([tb(gu[e]) for e in range(E)]))
+        blk.experts.down_proj.copy_(torch.stack([tb(dn[e]) for e in range(E)]))
+        blk.gate.weight.copy_(tb(wg))
+        if sh is not None:
+            blk.shared_expert.gate_proj.weight.copy_(tb(sh[0]))
+            blk.shared_expert.up_proj.weight.copy_(tb(sh[1]))
+            blk.shared_expert.down_proj.weight.copy_(tb(sh[2]))
+            blk.shared_expert_gate.weight.copy_(tb(sh[3]).reshape(1, -1))
+
+
+@pytest.mark.parametrize("T", [2, 16, 40])
+def test_prefill_matches_transformers_eager_experts(T):
+    """transformers' eager Qwen3_5MoeExperts.forward is the loop the reference restates (channel.py:44-60)."""
+    H, E, I, k = 128, 8, 64, 4
+    gu, dn, wg, _ = _layer(T, H, E, I)
+    blk = _tf_block(H, E, I, k, 64)
+    _load_tf_block(blk, gu, dn, wg, None)
+    x = bf16.to_f32(rng.tensor_bf16(T, rng.KIND_X, (T, H), 1.0))
+    ids, w, _ = moe.router_topk(moe.router_logits(x, wg), k)
+    with torch.no_grad():
+        ref = blk.experts(tb(x), torch.from_numpy(ids), tb(w)).float().numpy()
+    got = moe.experts_prefill(x, ids, w, gu, dn, E)
+    assert rel_l2(got, ref) <= 1e-3 and np.max(np.abs(got - ref)) <= 2e-2
+    assert np.mean(got == ref) >= 0.95
+
+
+def test_block_composition_matches_transformers():
+    """Shared MLP, sigmoid gate and the routed-first final add (modeling_qwen3_5_moe.py:787-798)."""
+    H, E, I, k, Is, T = 128, 8, 64, 2, 64, 12
+    gu, dn, wg, sh = _layer(21, H, E, I, Is)
+    blk = _tf_block(H, E, I, k, Is)
+    _load_tf_block(blk, gu, dn, wg, sh)
+    x = bf16.to_f32(rng.tensor_bf16(21, rng.KIND_X, (T, H), 1.0))
+    with torch.no_grad():
+        ref = blk(tb(x).reshape(1, T, H)).reshape(T, H).float().numpy()
+        _, tw, ti = blk.gate(tb(x))                      # the module's own (bf16-logit) routing
+    routed = moe.experts_prefill(x, ti.numpy(), tw.float().numpy(), gu, dn, E)
+    got = moe.add_bf16(routed, moe.shared_expert(x, *sh))
+    assert rel_l2(got, ref) <= 1e-3 and np.max(np.abs(got - ref)) <= 2e-2
+    with torch.no_grad():
+        s_ref = (torch.sigmoid(blk.shared_expert_gate(tb(x))) * blk.shared_expert(tb(x))).float().numpy()
+    assert rel_l2(moe.shared_expert(x, *sh), s_ref) <= 1e-3
+
+
+# ------------------------------------------------------------------ int4
+
+def test_dequant_exhaustive_codes_times_all_bf16_scales():
+    """16 codes x every finite bf16 scale vs torch ``q.to(bf16) * scale`` (channel_q4.py:14 with dtype bf16)."""
+    sb = np.arange(1 << 16, dtype=np.uint16)
+    s = bf16.to_f32(sb)
+    sb = sb[np.isfinite(s)]
+    packed = np.repeat(np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4), 1)[None, :]
+    packed = np.repeat(packed, sb.size, axis=0)                # [n_scales, 16] -> K = 32
+    scales = sb[:, None]                                       # group = K = 32
+    got = int4.dequant(packed, scales, group=32)
+    q = torch.from_numpy(int4.codes(packed)).to(torch.int16)   # int16 codes like channel_q4.py:11-12
+    want = (q.to(BF) * torch.from_numpy(bf16.to_f32(scales)).to(BF)).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_codes_nibble_order_matches_reference_dequant():
+    """Low nibble -> even k, high nibble -> odd k (moe_kernel.py:110-114 restated in torch)."""
+    g = np.random.default_rng(1)
+    packed = g.integers(0, 256, (8, 16), dtype=np.uint8)
+    p = torch.from_numpy(packed)
+    lo = (p & 0xF).to(torch.int16) - 8
+    hi = ((p >> 4) & 0xF).to(torch.int16) - 8
+    q = torch.stack([lo, hi], dim=-1).reshape(p.shape[0], -1)
+    assert np.array_equal(int4.codes(packed), q.numpy())
+
+
+def test_quantizer_invariants():
+    w = bf16.to_f32(rng.tensor_bf16(9, rng.KIND_GATE_UP, (64, 512), 0.02))
+    w[3, :128] = 0.0                                             # an all-zero group
+    packed, sb = int4.quantize(w, 128)
+    q = int4.codes(packed)
+    s = np.repeat(bf16.to_f32(sb), 128, axis=-1)
+    assert q.min() >= -7 and q.max() <= 7                        # s = max/7 never needs -8
+    assert np.all(q[3, :128] == 0) and np.all(bf16.to_f32(sb)[3, 0] == 0)
+    wh = bf16.to_f32(int4.dequant(packed, sb, 128))
+    assert np.all(np.abs(w - q * s) <= s / 2 * (1 + 2.0 ** -7) + 1e-30)
+    assert np.all(np.abs(wh - q * s) <= np.abs(q * s) * 2.0 ** -8)
+    # exactly representable inputs round-trip
+    s0 = np.float32(0.015625)
+    qq = np.tile(np.arange(-7, 8, dtype=np.float32), 9)[:128]
+    qq[0] = 7
+    p2, s2 = int4.quantize((qq * s0)[None, :], 128)
+    assert np.array_equal(int4.codes(p2)[0], qq.astype(np.int32))
+
+
+def test_int4_ffn_reference_known_answer_criterion():
+    """moe_kernel.py:128-145: random packed weights, fp16-like per-row scales, pass if max|err|/max|ref| < 2e-2.
+
+    Group = K reproduces the reference's per-row scale; the reference _ref_ffn
+    (moe_kernel.py:117-125) is restated in torch fp64.
+    """
+    torch.manual_seed(0)
+    E, H, I = 4, 256, 128
+    g = np.random.default_rng(0)
+    gup = g.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    dp = g.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    gus = bf16.bits(g.standard_normal((E, 2 * I, 1)).astype(np.float32) * 0.02)
+    ds = bf16.bits(g.standard_normal((E, H, 1)).astype(np.float32) * 0.02)
+    x = bf16.rnd(g.standard_normal(H).astype(np.float32) * 0.5)
+    rw = bf16.rnd(torch.softmax(torch.randn(E), 0).numpy())
+    out = torch.zeros(H, dtype=torch.float64)
+    for e in range(E):
+        gw = torch.from_numpy(int4.codes(gup[e])).double() * torch.from_numpy(bf16.to_f32(gus[e])).double()
+        dw = torch.from_numpy(int4.codes(dp[e])).double() * torch.from_numpy(bf16.to_f32(ds[e])).double()
+        gu_ = gw @ torch.from_numpy(x).double()
+        gg, uu = gu_.chunk(2)
+        out += float(rw[e]) * (dw @ (F.silu(gg) * uu))
+    ref = out.numpy()
+    got = _ffn_rowscale(x, gup, gus, dp, ds, rw)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 2e-2
+
+
+def _ffn_rowscale(x, gup, gus, dp, ds, rw):
+    """oracle int4.ffn with one scale per row: group = K for each projection."""
+    E = gup.shape[0]
+    y = np.zeros(x.shape[0], np.float64)
+    for e in range(E):
+        gu = int4.gemv_f32(gup[e], gus[e], x, group=gup.shape[2] * 2).astype(np.float64)
+        inter = gu.shape[0] // 2
+        gg, uu = gu[:inter], gu[inter:]
+        act = bf16.rnd(((gg / (1 + np.exp(-gg))) * uu).astype(np.float32))
+        d = int4.gemv_f32(dp[e], ds[e], act, group=dp.shape[2] * 2).astype(np.float64)
+        y = (y + (d * float(rw[e])).astype(np.float32)).astype(np.float32).astype(np.float64)
+    return bf16.rnd(y.astype(np.float32))
+
+
+def test_int4_ffn_group_form_equals_rowscale_form_when_scales_repeat():
+    """With every group scale of a row equal, the group-128 ffn equals the per-row form exactly."""
+    g = np.random.default_rng(3)
+    E, H, I = 2, 256, 128
+    gup = g.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    dp = g.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    gus = bf16.bits(g.standard_normal((E, 2 * I, 1)).astype(np.float32) * 0.02)
+    ds = bf16.bits(g.standard_normal((E, H, 1)).astype(np.float32) * 0.02)
+    x = bf16.rnd(g.standard_normal(H).astype(np.float32))
+    rw = bf16.rnd(np.array([0.6, 0.4], np.float32))
+    a = _ffn_rowscale(x, gup, gus, dp, ds, rw)
+    b = int4.ffn(x, [(gup[e], np.repeat(gus[e], 2, -1), dp[e], ds[e]) for e in range(E)], rw, group=128)
+    assert rel_l2(a, b) < 1e-6
