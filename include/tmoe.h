@@ -45,6 +45,7 @@ enum tmoe_status {
   TMOE_ERR_WORKSPACE = -4,  /* workspace smaller than tmoe_workspace_bytes()       */
   TMOE_ERR_HIP = -5,        /* a HIP runtime call or kernel launch failed          */
   TMOE_ERR_EXPERT_ID = -6,  /* device saw an expert id outside [0, E] (sentinel E is skipped) */
+  TMOE_ERR_TIMEOUT = -7,    /* a kernel's bounded dependency wait expired (results invalid)   */
 };
 
 /* ABI version of the loaded library (TMOE_ABI_VERSION at build time). */
@@ -58,7 +59,7 @@ const char* tmoe_strerror(int status);
 size_t tmoe_workspace_bytes(int T, int H, int E, int I, int k, int Is);
 
 /* Synchronise `stream`, then return and clear the device-side status the
- * kernels recorded in `workspace` (TMOE_OK or TMOE_ERR_EXPERT_ID). */
+ * kernels recorded in `workspace` (TMOE_OK, TMOE_ERR_EXPERT_ID or TMOE_ERR_TIMEOUT). */
 int tmoe_workspace_status(void* workspace, void* stream);
 
 /* ---------------------------------------------------------------- seeded data

@@ -1,10 +1,13 @@
 // extern "C" entry points: argument validation, workspace carving, launches.
+#include <stdlib.h>
+
 #include "tmoe_device.h"
 #include "tmoe_ws.h"
 #include "tmoe_decode.h"
 
 namespace tmoe {
 int decode_launch(DecodeParams& p, bool run_router, hipStream_t s);
+int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s);
 int launch_router_logits(const uint16_t* x, const uint16_t* wg, int T, int H, int E, float* logits, hipStream_t s);
 int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64, uint16_t* wb, int32_t* ids32,
                        float* wf, uint32_t* heat, hipStream_t s);
@@ -17,6 +20,20 @@ int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, fl
 
 
 using namespace tmoe;
+
+// Batch-1 path: the fused persistent kernel unless TMOE_DECODE_UNFUSED=1 (the
+// three-launch path, kept for comparison) or the shape has no fused variant.
+static int decode(DecodeParams& p, bool run_router, hipStream_t s) {
+  static const bool unfused = [] {
+    const char* v = getenv("TMOE_DECODE_UNFUSED");
+    return v && v[0] == '1';
+  }();
+  if (!unfused) {
+    const int st = decode_fused_launch(p, run_router, s);
+    if (st != TMOE_ERR_SHAPE) return st;
+  }
+  return decode_launch(p, run_router, s);
+}
 
 static bool misaligned(const void* p) { return ((uintptr_t)p & 15u) != 0; }
 
@@ -39,6 +56,7 @@ extern "C" const char* tmoe_strerror(int status) {
     case TMOE_ERR_WORKSPACE: return "workspace smaller than tmoe_workspace_bytes()";
     case TMOE_ERR_HIP: return "HIP runtime call or kernel launch failed";
     case TMOE_ERR_EXPERT_ID: return "expert id outside [0, num_experts] seen on the device";
+    case TMOE_ERR_TIMEOUT: return "a bounded device-side dependency wait expired";
     default: return "unknown tmoe status";
   }
 }
@@ -57,7 +75,7 @@ extern "C" int tmoe_workspace_status(void* workspace, void* stream) {
   if (!flags) return TMOE_OK;
   const uint32_t zero = 0;
   if (hipMemcpy(workspace, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess) return TMOE_ERR_HIP;
-  return TMOE_ERR_EXPERT_ID;
+  return (flags & kErrTimeout) ? TMOE_ERR_TIMEOUT : TMOE_ERR_EXPERT_ID;
 }
 
 static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
@@ -69,6 +87,11 @@ static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
   p.act_ws = ws_ptr<uint16_t>(ws, L.act);
   p.sact_ws = ws_ptr<uint16_t>(ws, L.act) + (size_t)p.k * p.I;
   p.sh_ws = ws_ptr<uint16_t>(ws, L.sh);
+  p.dbuf = ws_ptr<uint16_t>(ws, L.dbuf);
+  p.sync = ws_ptr<uint32_t>(ws, L.sync);
+  p.lg64 = ws_ptr<uint64_t>(ws, L.tagged);
+  p.act64 = p.lg64 + (p.E + 1);
+  p.dq64 = p.act64 + ((size_t)p.k * p.I + p.Is) / 2;
 }
 
 extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
@@ -89,7 +112,7 @@ extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* id
     p.H = H; p.E = E; p.I = I; p.k = k; p.Is = 0;
     p.out = (uint16_t*)out;
     bind_ws(p, workspace, L);
-    return decode_launch(p, false, s);
+    return decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
                         nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s);
@@ -127,7 +150,7 @@ extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, c
     p.w_out = (uint16_t*)weights_out;
     p.heat = heat;
     bind_ws(p, workspace, L);
-    return decode_launch(p, true, s);
+    return decode(p, true, s);
   }
   // T > 1: router, shared gate, then the prefill experts path with the shared expert as an extra group.
   float* logits = ws_ptr<float>(workspace, L.logits);

@@ -36,10 +36,13 @@ __device__ __forceinline__ float rbf16(float f) { return bf16_to_f32(f32_to_bf16
 
 // 16-byte global loads.  Weight streams are read exactly once per call, so they
 // carry the non-temporal hint; small shared vectors (x, activations) do not.
+// Pointers read from expert tables are generic; the casts keep these global_load
+// (not flat_load) instructions.
+typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
 __device__ __forceinline__ u32x4 ld_stream(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return __builtin_nontemporal_load((g_u32x4*)p);
 }
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(g_u32x4*)p; }
 
 // Dot of 8 bf16 weights (packed in 4 dwords) with 8 fp32 activations.
 __device__ __forceinline__ float dot8(const u32x4 w, const float* x, float acc) {

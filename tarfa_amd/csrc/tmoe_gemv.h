@@ -64,34 +64,24 @@ struct TopkOut {
   uint32_t* heat;    // [E] or null
 };
 
-template <int MAXEPL>
-__device__ __forceinline__ void wave_topk(const float* src, bool coherent, int E, int k, int lane, const TopkOut& o) {
-  float v[MAXEPL];
-#pragma unroll
-  for (int i = 0; i < MAXEPL; ++i) {
-    const int e = lane + 64 * i;
-    float val = -INFINITY;
-    if (e < E) val = coherent ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : src[e];
-    v[i] = val;
-  }
-  float lm = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < MAXEPL; ++i) lm = fmaxf(lm, v[i]);
-  const float m = wave_max(lm);
-  float ls = 0.f;
-#pragma unroll
-  for (int i = 0; i < MAXEPL; ++i)
-    if (lane + 64 * i < E) ls += expf(v[i] - m);
-  const float S = wave_sum(ls);
+// Selection and weights only, uniform across the wave (every lane holds them):
+// id[r] (E for an unselectable slot) and w[r] (the bf16 weight as fp32), r < k.
+struct NoPublish {
+  __device__ __forceinline__ void operator()(int, int) const {}
+};
 
+// v[i] = logit of expert lane + 64 i (-inf past E).  Selection rounds run first
+// (on_select(r, id) is called, wave-uniformly, as soon as slot r is known); the
+// softmax denominator and the renormalised weights follow.
+template <int MAXEPL, int MAXK, typename OnSelect = NoPublish>
+__device__ __forceinline__ void wave_topk_values(const float (&v)[MAXEPL], int E, int k, int lane, int (&id)[MAXK],
+                                                 float (&w)[MAXK], OnSelect on_select = OnSelect()) {
   uint32_t sel = 0;
-  float p[16];
-  int id[16];
-  float psum = 0.f;
+  float lw[MAXK];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    id[r] = INT_MAX;
-    p[r] = 0.f;
+  for (int r = 0; r < MAXK; ++r) {
+    id[r] = E;
+    lw[r] = -INFINITY;
     if (r >= k) continue;                         // k is wave-uniform
     float bv = -INFINITY;
     int bi = INT_MAX;
@@ -102,23 +92,69 @@ __device__ __forceinline__ void wave_topk(const float* src, bool coherent, int E
     }
     const float g = wave_max(bv);
     const int win = wave_min_int((bi != INT_MAX && bv == g) ? bi : INT_MAX);
-    if (win != INT_MAX && (win & 63) == lane) sel |= 1u << (win >> 6);
-    id[r] = win;
-    p[r] = (win == INT_MAX) ? 0.f : expf(g - m) / S;
+    if (win != INT_MAX) {
+      if ((win & 63) == lane) sel |= 1u << (win >> 6);
+      id[r] = win;
+      lw[r] = g;
+    }
+    on_select(r, id[r]);
+  }
+  // Softmax over all E in fp32, max-subtracted (the max is the first selection).
+  const float m = lw[0];
+  float ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXEPL; ++i)
+    if (lane + 64 * i < E) ls += expf(v[i] - m);
+  const float S = wave_sum(ls);
+  float p[MAXK];
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < MAXK; ++r) {
+    p[r] = (r < k && id[r] != E) ? expf(lw[r] - m) / S : 0.f;
     psum += p[r];
+  }
+#pragma unroll
+  for (int r = 0; r < MAXK; ++r) w[r] = (r < k && id[r] != E) ? rbf16(p[r] / psum) : 0.f;
+}
+
+template <int MAXEPL, int MAXK>
+__device__ __forceinline__ void wave_topk_select(const float* src, int E, int k, int lane, int (&id)[MAXK],
+                                                 float (&w)[MAXK]) {
+  float v[MAXEPL];
+#pragma unroll
+  for (int i = 0; i < MAXEPL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? src[e] : -INFINITY;
+  }
+  wave_topk_values<MAXEPL, MAXK>(v, E, k, lane, id, w);
+}
+
+template <int MAXEPL>
+__device__ __forceinline__ void wave_topk(const float* src, bool coherent, int E, int k, int lane, const TopkOut& o) {
+  int id[16];
+  float w[16];
+  if (coherent) {
+    float v[MAXEPL];
+#pragma unroll
+    for (int i = 0; i < MAXEPL; ++i) {
+      const int e = lane + 64 * i;
+      v[i] = e < E ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+    }
+    wave_topk_values<MAXEPL, 16>(v, E, k, lane, id, w);
+  } else {
+    wave_topk_select<MAXEPL, 16>(src, E, k, lane, id, w);
   }
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (r >= k) continue;
-      const bool ok = id[r] != INT_MAX;
-      const int e = ok ? id[r] : E;                 // unselectable -> the skip sentinel E
-      const uint16_t wb = ok ? f32_to_bf16(p[r] / psum) : (uint16_t)0;
+      const int e = id[r];
+      const uint16_t wb = f32_to_bf16(w[r]);
       if (o.ids32) o.ids32[r] = e;
-      if (o.wf) o.wf[r] = bf16_to_f32(wb);
+      if (o.wf) o.wf[r] = w[r];
       if (o.ids64) o.ids64[r] = e;
       if (o.wb) o.wb[r] = wb;
-      if (o.heat && ok) atomicAdd(o.heat + e, 1u);
+      if (o.heat && e < E) atomicAdd(o.heat + e, 1u);
     }
   }
 }

@@ -8,13 +8,39 @@
 namespace tmoe {
 
 enum StatusSlot {
-  kStatusError = 0,      // OR of device-detected error bits (bit 0: expert id out of range)
-  kStatusRouterDone = 1, // arrival counter of the decode router blocks
+  kStatusError = 0,      // OR of device-detected error bits (kErrExpertId | kErrTimeout)
+  kStatusRouterDone = 1, // arrival counter of the unfused decode router blocks
   kStatusSlots = 64,
 };
+enum ErrorBit { kErrExpertId = 1u, kErrTimeout = 2u };
+
+// Synchronisation lines of the fused decode task graph.  Every counter owns a
+// 256-byte line (64 uint32): atomics on one hot line serialise at ~11 ns each.
+// All are zero between calls: the last row-block combine of a call re-zeroes the
+// task-graph lines, and the last block to leave a queue re-zeroes that queue's lines.
+constexpr int kLine = 64;                 // uint32 per line
+constexpr int kMaxSlots = 16;             // top-k
+constexpr int kMaxRowBlocks = 128;        // H / 32
+constexpr int kRouteReplicas = 32;        // routing published to this many lines
+// Tagged hand-off words of the fused decode: a value and its valid tag travel in
+// one coherent store, so a consumer polls the data itself.  Zero = not written.
+constexpr uint32_t kTag16 = 0xA5A5u;      // high half of a 32-bit routing word (payload: low 16 bits)
+constexpr uint32_t kTag32 = 0x5A5A5A5Au;  // high word of a 64-bit logit / activation / shared-down word
+constexpr int kQueues = 8;                // task queues (one per XCD-sized group of blocks)
+enum SyncLine {
+  kLnCombined = 0,                        // row blocks combined
+  kLnQueue = 1,                           // [kQueues] next draw index per queue
+  kLnQueueExit = kLnQueue + kQueues,      // [kQueues] blocks that left each queue
+  kLnRowDone = kLnQueueExit + kQueues,    // [kMaxRowBlocks] down tasks finished per row block
+  kLnRoute = kLnRowDone + kMaxRowBlocks,  // [kRouteReplicas]: tagged {gate, ids[16], w[16]}
+  kSyncLines = kLnRoute + kRouteReplicas,
+};
+// Word offsets inside a route replica line.
+enum RouteWord { kRwGate = 0, kRwIds = 1, kRwW = 1 + kMaxSlots };
 
 struct Ws {
-  size_t status;   // uint32[64]
+  size_t status;   // uint32[kStatusSlots]
+  size_t sync;     // uint32[kSyncLines * kLine]   fused decode task-graph lines
   size_t logits;   // f32[T * (E + 1)]   router logits; column E = shared-gate logit (decode)
   size_t ids;      // int32[T * k]
   size_t wts;      // f32[T * k]         routing weights (bf16 values)
@@ -26,6 +52,9 @@ struct Ws {
   size_t inv;      // int32[T * k]
   size_t scratch;  // int32[E + 64]      dispatch counters
   size_t ch;       // bf16[T * k * H]    weighted per-assignment expert outputs (T > 1)
+  size_t dbuf;     // bf16[(k + 1) * H]  per-expert down outputs of the fused decode (T == 1)
+  size_t tagged;   // u64[(E + 1) + (k * I + Is) / 2 + (k + 1) * H / 2]  tagged logits, activation
+                   // pairs, per-slot down pairs (slot k = shared expert)
   size_t total;
 };
 
@@ -38,6 +67,7 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   const size_t inter = (size_t)(I > Is ? I : Is);
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   w.status = take(sizeof(uint32_t) * kStatusSlots);
+  w.sync = take(sizeof(uint32_t) * kSyncLines * kLine);
   w.logits = take(sizeof(float) * t * (size_t)(E + 1));
   w.ids = take(sizeof(int32_t) * t * (size_t)k);
   w.wts = take(sizeof(float) * t * (size_t)k);
@@ -49,6 +79,8 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.inv = take(sizeof(int32_t) * t * (size_t)k);
   w.scratch = take(sizeof(int32_t) * (size_t)(E + 64));
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
+  w.dbuf = take(2 * (size_t)(k + 1) * (size_t)H);
+  w.tagged = take(8 * ((size_t)(E + 1) + ((size_t)k * I + (size_t)Is) / 2 + (size_t)(k + 1) * H / 2));
   w.total = o;
   return w;
 }
