@@ -11,8 +11,9 @@
  *     Conditions the device detects (an expert id outside [0, E]) are recorded
  *     in the workspace and reported by tmoe_workspace_status().
  *   - Nothing here allocates device memory.  Callers pass a workspace of at
- *     least tmoe_workspace_bytes(...) bytes, ZERO-FILLED before its first use;
- *     the kernels leave its counters zeroed again.  Calls that share one
+ *     least tmoe_workspace_bytes(...) bytes, ZERO-FILLED before its first use
+ *     and not written by the caller afterwards: the kernels return its counters
+ *     to zero and keep a call counter (epoch) in it.  Calls that share one
  *     workspace must be ordered (same stream, or joined with events).
  *   - Expert weights are reached through a device "expert table":
  *       bf16 table  uint64_t[E][2] = { gate_up [2I, H], down [H, I] } base pointers

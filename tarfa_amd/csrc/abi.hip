@@ -78,7 +78,7 @@ extern "C" int tmoe_workspace_status(void* workspace, void* stream) {
   return (flags & kErrTimeout) ? TMOE_ERR_TIMEOUT : TMOE_ERR_EXPERT_ID;
 }
 
-static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
+static void bind_ws(DecodeParams& p, void* ws, size_t ws_bytes, const Ws& L) {
   p.status = ws_ptr<uint32_t>(ws, L.status);
   p.logits_ws = ws_ptr<float>(ws, L.logits);
   p.ids_ws = ws_ptr<int32_t>(ws, L.ids);
@@ -87,11 +87,12 @@ static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
   p.act_ws = ws_ptr<uint16_t>(ws, L.act);
   p.sact_ws = ws_ptr<uint16_t>(ws, L.act) + (size_t)p.k * p.I;
   p.sh_ws = ws_ptr<uint16_t>(ws, L.sh);
-  p.dbuf = ws_ptr<uint16_t>(ws, L.dbuf);
   p.sync = ws_ptr<uint32_t>(ws, L.sync);
   p.lg64 = ws_ptr<uint64_t>(ws, L.tagged);
   p.act64 = p.lg64 + (p.E + 1);
   p.dq64 = p.act64 + ((size_t)p.k * p.I + p.Is) / 2;
+  p.handoff = ws_ptr<void>(ws, L.logits);
+  p.handoff_words = (ws_bytes - L.logits) / 8;
 }
 
 extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
@@ -111,7 +112,7 @@ extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* id
     p.w_in = (const uint16_t*)weights;
     p.H = H; p.E = E; p.I = I; p.k = k; p.Is = 0;
     p.out = (uint16_t*)out;
-    bind_ws(p, workspace, L);
+    bind_ws(p, workspace, ws_bytes, L);
     return decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
@@ -149,7 +150,7 @@ extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, c
     p.ids_out = ids_out;
     p.w_out = (uint16_t*)weights_out;
     p.heat = heat;
-    bind_ws(p, workspace, L);
+    bind_ws(p, workspace, ws_bytes, L);
     return decode(p, true, s);
   }
   // T > 1: router, shared gate, then the prefill experts path with the shared expert as an extra group.

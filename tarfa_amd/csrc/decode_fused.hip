@@ -1,37 +1,48 @@
-// Batch-1 (decode) MoE layer as ONE persistent kernel over eight dependency-ordered task queues.
+// Batch-1 (decode) MoE layer as ONE persistent kernel whose waves draw tasks from
+// 32 dependency-ordered queues.
 //
-// Tasks (each one block of 4 waves), in list order:
-//   R   router rows: fp32 logits, 1 row per wave, and the shared-gate logit
+// Tasks (each one wave), in list order:
+//   R   router rows: fp32 logits, 4 rows per task (row E = the shared-gate logit)
 //   K   gather every logit, top-k, publish the routing   (needs: all R)
-//   S   shared expert gate/up pairs -> bf16 SwiGLU activations
-//   SD  shared expert down, 32 rows                    (needs: the shared activations)
-//   Gj  routed gate/up pairs of slot j -> activations   (needs: slot j's expert id)
-//   Dj  routed down of slot j, 32 rows                  (needs: slot j's activations)
+//   S   shared expert gate/up, 2 row pairs -> 2 bf16 SwiGLU activations
+//   SD  shared expert down, 8 rows                     (needs: every S)
+//   Gj  routed gate/up of slot j, 2 row pairs          (needs: slot j's expert id)
+//   Dj  routed down of slot j, 8 rows                  (needs: every Gj)
 //       D(k-1), last in the list, also combines its rows from every slot's tagged
 //       results: acc = bf16(acc + bf16(w_j * d_j)) in router order, then
 //       acc = bf16(acc + bf16(gate * d_shared)), and writes the output.
-// ordered R, K, S, SD, G0 .. G(L), then D(j-L) after each later Gj, then the
-// remaining D (L = kDownLag): the shared expert streams while the router resolves,
-// and a slot's down rows are drawn only once its gate/up tasks have had time to
-// finish (about one resident grid of tasks later).  K publishes each expert id as
-// soon as its selection round ends, so G0 starts before the top-k is complete.
+// ordered R, K, G0 .. G(L), then D(j-L) after each later Gj (L = kDownLag), S
+// after G(kSharedAfter) and SD L slots later, then the remaining D: while the
+// routing resolves only the router rows load, and down rows are drawn only once
+// their gate/up tasks have had time to finish.  K keeps its vector-memory
+// instructions few (a wave's store waits behind every load queued on its CU):
+// 5 loads, then the whole routing in 3 stores.
 //
-// Hand-offs are built around two measured MI355X costs: a memory round trip under
-// streaming load is ~3 us, and atomics on one hot 256-B line serialise at ~11 ns.
-//   - Logits, routing and activations travel as TAGGED words: value and valid tag in
-//     one device-coherent store (relaxed agent-scope atomics bypass the per-XCD L2
-//     copies), so a consumer polls the data itself -- one round trip per hand-off,
-//     no store-completion wait, no counter, no cache-wide write-back / invalidate.
-//   - Only the row-block combine counts arrivals (one 256-B line per row block).
-//   - Blocks draw tasks from eight queue counters (block b uses queue b % 8, which
-//     serves tasks b % 8, +8, +16, ...).  A task only waits on tasks with smaller
-//     indices and a block only draws from its own queue, so the smallest unfinished
-//     task is always held, or next to be drawn, by a running block: blocks 0..7 (one
-//     per queue) are dispatched first and keep drawing until their queue is empty.
-//     (A cooperative launch would also guarantee residency, at ~20 us per call.)
-//   - Every poll backs off exponentially and is bounded (kErrTimeout on expiry).
-//   - The last combine of a call re-zeroes every tagged word and counter; the last
-//     block to leave a queue re-zeroes that queue's lines.
+// Hand-offs are built around measured MI355X costs: a memory round trip under
+// streaming load is several us, atomics on one hot 256-B line serialise at ~11 ns,
+// and every poll of a coherent word travels to the memory side like the weight
+// stream itself, so polling must be cheap.
+//   - Logits, routing, activations and per-slot down rows travel as TAGGED 64-bit
+//     words {payload, tag}: one device-coherent store (relaxed agent-scope atomics
+//     bypass the per-XCD L2 copies), so a consumer checks the data itself -- no
+//     store-completion wait, no cache-wide write-back / invalidate.
+//     The tag is the call's epoch (a counter in the workspace, advanced when a
+//     call ends), so words left by earlier calls never match and nothing is
+//     cleared between calls; at the 2^32 wrap the ending wave zeroes the hand-off area.
+//   - A down task reads its activations with plain loads issued together with its
+//     weight rows (queued kDownLag slots after its gate/up tasks, the activations
+//     are normally complete); stale words are re-polled with coherent loads.
+//   - Each wave caches the routing it has seen (lane l: slot l's expert), so only
+//     its first task of a slot waits for the id.
+//   - Queue q (of 32) is served by wave q % 4 of the blocks b with b % 8 == q / 4
+//     (one XCD) and holds tasks q, q + 32, ...; the wave of rank r = b / 8 among
+//     its queue's `users` takes tickets r, r + users, r + 2 users, ...  Each wave
+//     runs its tasks in increasing order, a task only waits on tasks with smaller
+//     indices, and the grid fits on the GPU at once, so the smallest unfinished
+//     task is always some running wave's current task and can finish.
+//   - Every poll backs off and is bounded (kErrTimeout on expiry).
+//   - The last wave to leave a queue re-zeroes its exit count; the last queue to
+//     drain advances the epoch.
 // Reference: tarfa/engine/fused_int4.py:163-205; transformers/.../modeling_qwen3_5_moe.py:715-717, 768-798.
 #include <mutex>
 
@@ -41,13 +52,16 @@
 
 namespace tmoe {
 
-constexpr int kFPairsPerWave = 2;      // gate/up pairs per wave (4 rows of K = H in flight)
-constexpr int kFPairsPerTask = 4 * kFPairsPerWave;
-constexpr int kFDownRowsPerWave = 8;   // down rows per wave (8 rows of K = I in flight)
-constexpr int kFDownRowsPerTask = 4 * kFDownRowsPerWave;
+constexpr int kWaves = 4;              // waves per block
+constexpr int kRouterRows = 4;         // router rows per R task
+constexpr int kPairs = 2;              // gate/up row pairs per G / S task (4 rows of K = H in flight)
+constexpr int kDownRows = 8;           // down rows per D / SD task (8 rows of K = I in flight)
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 3;            // Dj is queued after G(j + kDownLag)
+constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
+constexpr int kBlocksPerCU = 2;        // resident blocks per CU (bounds the bytes in flight per XCD)
 constexpr uint32_t kSpinLimit = 1u << 20;   // polls, each >= 64 cycles apart: never reached by a healthy graph
+static_assert(kQueues == 8 * kWaves, "queue q is served by wave q % 4 of the blocks b with b % 8 == q / 4");
 
 enum TaskType { kTR, kTK, kTS, kTSD, kTG, kTD };
 
@@ -63,17 +77,28 @@ __device__ __forceinline__ uint64_t ld64c(const uint64_t* p) {
 __device__ __forceinline__ void st64c(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint64_t tag64(uint32_t v) { return ((uint64_t)kTag32 << 32) | v; }
-__device__ __forceinline__ bool tagged64(uint64_t w) { return (uint32_t)(w >> 32) == kTag32; }
-__device__ __forceinline__ uint32_t tag32(uint32_t payload16) { return (kTag16 << 16) | (payload16 & 0xFFFFu); }
-__device__ __forceinline__ bool tagged32(uint32_t w) { return (w >> 16) == kTag16; }
-
-// Every store this wave issued has completed (gfx9 counts stores in vmcnt).
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ uint32_t add32c(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A wave-uniform load of memory that no task writes during the call (expert
+// table, caller-supplied routing): through the constant address space it is a
+// scalar load, so waiting for it never waits for this wave's outstanding
+// vector stores.
+template <typename T>
+__device__ __forceinline__ T ld_inv(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
+__device__ __forceinline__ bool has_tag(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 
 __device__ __forceinline__ uint32_t* line(const DecodeParams& p, int ln) { return p.sync + (size_t)ln * kLine; }
+__device__ __forceinline__ uint64_t* line64(const DecodeParams& p, int ln) {
+  return reinterpret_cast<uint64_t*>(line(p, ln));
+}
 
-// Exponential back-off between polls; false once the bound expires (flags kErrTimeout).
+// Back-off between polls, doubling up to s_sleep(MAXNAP); false once the bound
+// expires (flags kErrTimeout).
+template <int MAXNAP>
 struct Backoff {
   uint32_t n = 0, nap = 1;
   __device__ __forceinline__ bool step(uint32_t* err) {
@@ -82,169 +107,189 @@ struct Backoff {
     else if (nap <= 4) __builtin_amdgcn_s_sleep(4);
     else if (nap <= 8) __builtin_amdgcn_s_sleep(8);
     else __builtin_amdgcn_s_sleep(16);
-    nap = nap < 16 ? nap * 2 : 16;
+    nap = nap < MAXNAP ? nap * 2 : MAXNAP;
     if (++n < kSpinLimit) return true;
-    atomicOr(err, kErrTimeout);
+    if ((threadIdx.x & 63) == 0) atomicOr(err, kErrTimeout);
     return false;
   }
 };
 
-// Poll one tagged 32-bit word until it is written; returns its 16-bit payload
-// (or 0xFFFF after a timeout).
-__device__ __forceinline__ uint32_t poll_word(const uint32_t* w, uint32_t* err) {
-  Backoff b;
-  for (;;) {
-    const uint32_t v = ld32c(w);
-    if (tagged32(v)) return v & 0xFFFFu;
-    if (!b.step(err)) return 0xFFFFu;
-  }
-}
-
-// A wave polls the K / 2 tagged activation pairs at w until every one it needs is
-// written, and unpacks them into its fragment layout.
-template <int MAXC>
-__device__ __forceinline__ void poll_xfrag(XFrag<MAXC>& f, const uint64_t* w, int K, int lane, uint32_t* err) {
-  Backoff b;
-  for (;;) {
+// Read the K / 2 tagged activation pairs into a packed fragment (lane l: columns
+// c*512 + 8l .. +7).  The first read is a plain load issued together with the
+// caller's weight loads -- the producing gate/up tasks are normally long done,
+// and through the XCD's L2 one memory fetch serves every wave of the XCD; words
+// still carrying an old tag are re-read with coherent loads until they match.
+template <int MAXC, bool EXACT>
+__device__ __forceinline__ void load_acts(XPack<MAXC>& f, const uint64_t* w, int K, int lane, uint32_t tag,
+                                          uint32_t* err) {
+  {
     bool ok = true;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
       const int col = c * 512 + lane * 8;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint64_t v = 0;
-        if (col < K) {
-          v = ld64c(w + col / 2 + q);
-          ok = ok && tagged64(v);
-        }
-        f.v[c][2 * q] = bf16_lo((uint32_t)v);
-        f.v[c][2 * q + 1] = bf16_hi((uint32_t)v);
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      if (EXACT || col < K) {
+        lo = ld16(w + col / 2);
+        hi = ld16(w + col / 2 + 2);
+        ok &= lo.y == tag && lo.w == tag && hi.y == tag && hi.w == tag;
       }
+      f.v[c] = u32x4{lo.x, lo.z, hi.x, hi.z};
     }
     if (__all(ok)) return;
+  }
+  Backoff<4> b2;
+  for (;;) {
+    // All loads of a round issue before any is checked (addresses clamped, not skipped).
+    uint64_t v[MAXC][4];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[c][q] = ld64c(w + min(c * 512 + lane * 8, K - 8) / 2 + q);
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const bool in = EXACT || c * 512 + lane * 8 < K;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ok &= !in || has_tag(v[c][q], tag);
+      f.v[c] = in ? u32x4{(uint32_t)v[c][0], (uint32_t)v[c][1], (uint32_t)v[c][2], (uint32_t)v[c][3]}
+                  : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (__all(ok)) return;
+    if (!b2.step(err)) return;
+  }
+}
+
+__device__ __forceinline__ const uint64_t* route(const DecodeParams& p) {
+  return line64(p, kLnRoute + (int)(blockIdx.x % kRouteReplicas));
+}
+
+// The wave's routing cache: lane l < k holds slot l's route word {weight, id},
+// lane kRwGate the shared gate, once seen (kUnseenWord before).  A poll refreshes
+// every missing word at once until the lanes in `need` are all seen.
+constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
+
+__device__ __forceinline__ void route_poll(const DecodeParams& p, int lane, uint32_t& rwc, uint64_t need, uint32_t tag,
+                                           uint32_t* err) {
+  const bool mine = lane < p.k || (lane == kRwGate && p.sh_gate != nullptr);
+  const uint64_t* rt = route(p);
+  Backoff<16> b;
+  for (;;) {
+    if (mine && rwc == kUnseenWord) {
+      const uint64_t w = ld64c(rt + lane);
+      if (has_tag(w, tag)) rwc = (uint32_t)w;
+    }
+    if (!(__ballot(rwc == kUnseenWord) & need)) return;
     if (!b.step(err)) return;
   }
 }
 
-__device__ __forceinline__ const uint32_t* route(const DecodeParams& p) {
-  return line(p, kLnRoute + (int)(blockIdx.x % kRouteReplicas));
+// Expert of slot j (wave-uniform) for this wave, or -1 for a skipped or invalid id
+// (caller-supplied routing is in the cache from the start).
+__device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, int lane, uint32_t& rwc, uint32_t tag,
+                                                uint32_t* err) {
+  if (!p.ids_in && (uint32_t)__builtin_amdgcn_readlane((int)rwc, j) == kUnseenWord)
+    route_poll(p, lane, rwc, 1ull << j, tag, err);
+  const uint32_t w = (uint32_t)__builtin_amdgcn_readlane((int)rwc, j);
+  const int e = (int)(w & 0xFFFFu);
+  return (w != kUnseenWord && e < p.E) ? e : -1;
 }
 
-// Expert id of slot j for this block (thread 0 polls the routing when it comes
-// from the router), broadcast through LDS; -1 for a skipped or invalid id.
-__device__ __forceinline__ int block_slot_expert(const DecodeParams& p, int j, int* s_e, uint32_t* err) {
-  if (threadIdx.x == 0) {
-    const int e = p.ids_in ? (int)p.ids_in[j] : (int)poll_word(route(p) + kRwIds + j, err);
-    if (e < 0 || e > p.E) atomicOr(err, kErrExpertId);
-    *s_e = (e >= 0 && e < p.E) ? e : -1;
-  }
-  __syncthreads();
-  return *s_e;
-}
-
-// SwiGLU of gate/up row pairs [i0, i0+2): one tagged activation pair per wave.
-template <int MAXC>
+// SwiGLU of gate/up row pairs [i0, i0 + 2): one tagged activation pair.
+template <int MH, bool EXACT>
 __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* up, int i0, int n_rows, int K,
-                                         const uint16_t* x, int lane, uint64_t* act64) {
-  XFrag<MAXC> xf;
-  load_xfrag<MAXC>(xf, x, K, lane);
-  const uint16_t* rows[2 * kFPairsPerWave];
+                                         const uint16_t* x, int lane, uint64_t* act64, uint32_t tag) {
+  XPack<MH> xf;
+  load_xpack<MH, EXACT>(xf, x, K, lane);
+  const uint16_t* rows[2 * kPairs];
 #pragma unroll
-  for (int q = 0; q < kFPairsPerWave; ++q) {
+  for (int q = 0; q < kPairs; ++q) {
     const int i = min(i0 + q, n_rows - 1);
     rows[q] = gate + (size_t)i * K;
-    rows[kFPairsPerWave + q] = up + (size_t)i * K;
+    rows[kPairs + q] = up + (size_t)i * K;
   }
-  float d[2 * kFPairsPerWave];
-  wave_dots<MAXC, 2 * kFPairsPerWave>(rows, xf, K, lane, d);
-  static_assert(kFPairsPerWave == 2, "activations are published as one tagged bf16 pair per wave");
+  float d[2 * kPairs];
+  wave_dots_p<MH, 2 * kPairs, EXACT>(rows, xf, K, lane, d);
+  static_assert(kPairs == 2, "activations are published as one tagged bf16 pair per task");
   if (lane == 0) {
     const uint32_t a0 = f32_to_bf16(swiglu_bf16(rbf16(d[0]), rbf16(d[2])));
     const uint32_t a1 = (i0 + 1 < n_rows) ? f32_to_bf16(swiglu_bf16(rbf16(d[1]), rbf16(d[3]))) : 0u;
-    st64c(act64 + i0 / 2, tag64(a0 | (a1 << 16)));
+    st64c(act64 + i0 / 2, tagged(tag, a0 | (a1 << 16)));
   }
 }
 
-// 8 rows of one down projection per wave: d[r] = bf16(dot(w[h0 + r], act)).  The
-// weight rows are requested before the activations are polled, so the wait for
-// the producing gate/up tasks overlaps this task's own HBM traffic.
-template <int MAXC>
-__device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act64, int K, int H, int h0, int lane,
-                                          float (&d)[kFDownRowsPerWave], uint32_t* err) {
-  u32x4 wr[kFDownRowsPerWave][MAXC];
+// 8 rows of one down projection: d[r] = bf16(dot(w[h0 + r], act)).  The weight
+// rows and the activations are requested together: one round trip when the
+// producing gate/up tasks are done.
+template <int MI, bool EXACT>
+__device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act64, const DecodeParams& p, int K,
+                                          int h0, int lane, float (&d)[kDownRows], uint32_t tag, uint32_t* err) {
+  u32x4 wr[kDownRows][MI];
 #pragma unroll
-  for (int r = 0; r < kFDownRowsPerWave; ++r)
+  for (int r = 0; r < kDownRows; ++r)
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
+    for (int c = 0; c < MI; ++c) {
       const int col = c * 512 + lane * 8;
-      wr[r][c] = col < K ? ld_stream(w + (size_t)min(h0 + r, H - 1) * K + col) : u32x4{0u, 0u, 0u, 0u};
+      wr[r][c] = (EXACT || col < K) ? ld_stream(w + (size_t)min(h0 + r, p.H - 1) * K + col)
+                                    : u32x4{0u, 0u, 0u, 0u};
     }
-  XFrag<MAXC> af;
-  poll_xfrag<MAXC>(af, act64, K, lane, err);
+  XPack<MI> af;
+  load_acts<MI, EXACT>(af, act64, K, lane, tag, err);
 #pragma unroll
-  for (int r = 0; r < kFDownRowsPerWave; ++r) {
+  for (int r = 0; r < kDownRows; ++r) {
     float acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) acc = dot8(wr[r][c], af.v[c], acc);
+    for (int c = 0; c < MI; ++c) acc = dot8p(wr[r][c], af.v[c], acc);
     d[r] = rbf16(wave_sum(acc));
   }
 }
 
-// Lane 0 polls the 4 tagged pairs at w until each carries `want` in its high word.
-__device__ __forceinline__ void poll_pairs(const uint64_t* w, uint32_t want, uint32_t (&pair)[4], uint32_t* err) {
-  Backoff b;
-  for (;;) {
-    bool ok = true;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint64_t v = ld64c(w + q);
-      ok = ok && (uint32_t)(v >> 32) == want;
-      pair[q] = (uint32_t)v;
-    }
-    if (ok || !b.step(err)) return;
-  }
-}
-
-// The K task's wave 0: gather every tagged logit, select the top-k, publish the
-// routing.  Kept compact (rolled rounds, per-slot values in LDS, weights computed
-// one slot per lane): this runs once per call on a cold instruction cache while
-// the rest of the GPU streams, so code size is latency here.
+// The K task: gather every tagged logit, select the top-k, publish the routing.
+// Kept compact (rolled rounds, per-slot values held by lane r): this runs once
+// per call on a cold instruction cache while the rest of the GPU streams, so code
+// size is latency here.
 template <int MAXEPL>
-__device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane, uint32_t* err, int* s_id,
-                                                float* s_lw) {
+__device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane, uint32_t tag, uint32_t* err) {
   const bool has_sh = p.sh_gate != nullptr;
   __builtin_amdgcn_s_setprio(3);   // the routing gates every expert task: issue ahead of streaming waves
   float v[MAXEPL];
   float gl = 0.f;
-  Backoff b;
-  for (;;) {
-    bool ok = true;
+  if (p.logits_in) {
 #pragma unroll
     for (int i = 0; i < MAXEPL; ++i) {
       const int e = lane + 64 * i;
-      v[i] = -INFINITY;
-      if (e < p.E) {
-        if (p.logits_in) {
-          v[i] = p.logits_in[e];
-        } else {
-          const uint64_t w = ld64c(p.lg64 + e);
-          ok = ok && tagged64(w);
-          v[i] = __uint_as_float((uint32_t)w);
+      v[i] = e < p.E ? p.logits_in[min(e, p.E - 1)] : -INFINITY;
+    }
+  }
+  if (!p.logits_in || has_sh) {
+    // Every load of a poll round is issued before any is waited for: the
+    // addresses are clamped into the logit words, never skipped.
+    Backoff<1> b;
+    for (;;) {
+      uint64_t w[MAXEPL];
+#pragma unroll
+      for (int i = 0; i < MAXEPL; ++i) w[i] = ld64c(p.lg64 + min(lane + 64 * i, p.E - 1));
+      const uint64_t wg = ld64c(p.lg64 + p.E);
+      bool ok = !has_sh || has_tag(wg, tag);
+      gl = __uint_as_float((uint32_t)wg);
+      if (!p.logits_in) {
+#pragma unroll
+        for (int i = 0; i < MAXEPL; ++i) {
+          const bool in = lane + 64 * i < p.E;
+          ok &= !in || has_tag(w[i], tag);
+          v[i] = in ? __uint_as_float((uint32_t)w[i]) : -INFINITY;
         }
       }
+      if (__all(ok)) break;
+      if (!b.step(err)) break;
     }
-    if (has_sh) {
-      const uint64_t w = ld64c(p.lg64 + p.E);
-      ok = ok && tagged64(w);
-      gl = __uint_as_float((uint32_t)w);
-    }
-    if (__all(ok)) break;
-    if (!b.step(err)) break;
   }
-  // Selection rounds: logit descending, ties to the lower expert index.  Each id is
-  // published the moment its round ends, so slot 0's gate/up work starts at once.
-  uint32_t* rep = line(p, kLnRoute + (lane & (kRouteReplicas - 1)));
+  // Selection rounds: logit descending, ties to the lower expert index.  Lane r
+  // keeps slot r; nothing is stored until the routing is complete (a store waits
+  // behind the streaming loads queued on this CU).
   uint32_t sel = 0;
+  int my_id = p.E;          // lane r < k: slot r's expert and logit
+  float my_lw = -INFINITY;
+  float m = 0.f;            // the largest logit (slot 0)
 #pragma unroll 1
   for (int r = 0; r < p.k; ++r) {
     float bv = -INFINITY;
@@ -259,36 +304,44 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
     }
     const float g = wave_max(bv);
     const int win = wave_min_int((bi != INT_MAX && bv == g) ? bi : INT_MAX);
-    const int e = win == INT_MAX ? p.E : win;
     if (win != INT_MAX && (win & 63) == lane) sel |= 1u << (win >> 6);
-    if (lane < kRouteReplicas) st32c(rep + kRwIds + r, tag32((uint32_t)e));
-    if (lane == 0) {
-      s_id[r] = e;
-      s_lw[r] = g;
+    if (lane == r) {
+      my_id = win == INT_MAX ? p.E : win;
+      my_lw = g;
     }
+    if (r == 0) m = g;
   }
-  // Softmax over all E in fp32 (max-subtracted; the max is slot 0), renormalised
-  // over the k selected, rounded to bf16 -- one slot per lane.
-  const float m = s_lw[0];
+  // Softmax over all E in fp32 (max-subtracted), renormalised over the k
+  // selected, rounded to bf16 -- one slot per lane.
   float ls = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXEPL; ++i)
     if (lane + 64 * i < p.E) ls += expf(v[i] - m);
   const float S = wave_sum(ls);
   const bool mine = lane < p.k;
-  const int id = mine ? s_id[lane] : p.E;
-  const float pr = (mine && id < p.E) ? expf(s_lw[lane] - m) / S : 0.f;
+  const float pr = (mine && my_id < p.E) ? expf(my_lw - m) / S : 0.f;
   const float psum = wave_sum(pr);   // all lanes active: a DPP reduction must not run divergent
-  const float wr = (mine && id < p.E) ? rbf16(pr / psum) : 0.f;
-  if (mine) {
-    const uint32_t tw = tag32(f32_to_bf16(wr));
-#pragma unroll 1
-    for (int rr = 0; rr < kRouteReplicas; ++rr) st32c(line(p, kLnRoute + rr) + kRwW + lane, tw);
-    if (p.ids_out) p.ids_out[lane] = id;
-    if (p.w_out) p.w_out[lane] = f32_to_bf16(wr);
-    if (p.heat && id < p.E) atomicAdd(p.heat + id, 1u);
+  const float wr = (mine && my_id < p.E) ? rbf16(pr / psum) : 0.f;
+  const uint32_t wb = f32_to_bf16(wr);
+  // Route words: lane r < k holds slot r's {weight, id}; lane kRwGate the gate.
+  uint32_t word = ((uint32_t)wb << 16) | (uint32_t)my_id;
+  if (lane == kRwGate) word = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
+  // Replica i of kRouteReplicas gets words 0 .. kRouteWords-1; lane l writes word
+  // (it * 64 + l) of the flattened replicas.
+#pragma unroll
+  for (int it = 0; it < (kRouteReplicas * kRouteWords + 63) / 64; ++it) {
+    const int f = it * 64 + lane;
+    const int rw = f % kRouteWords;
+    const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(rw * 4, (int)word);
+    const bool used = rw < p.k || (rw == kRwGate && has_sh);
+    if (f < kRouteReplicas * kRouteWords && used)
+      st64c(line64(p, kLnRoute + f / kRouteWords) + rw, tagged(tag, v));
   }
-  if (lane < kRouteReplicas) st32c(rep + kRwGate, tag32(has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u));
+  if (mine) {
+    if (p.ids_out) p.ids_out[lane] = my_id;
+    if (p.w_out) p.w_out[lane] = wb;
+    if (p.heat && my_id < p.E) atomicAdd(p.heat + my_id, 1u);
+  }
   if (p.logits_out)
 #pragma unroll
     for (int i = 0; i < MAXEPL; ++i)
@@ -296,127 +349,104 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
   __builtin_amdgcn_s_setprio(0);
 }
 
-template <int MH>
-__device__ __forceinline__ void task_router(const DecodeParams& p, int t, int lane, int wid, uint32_t* err) {
+// Router rows [4t, 4t + 4) of E + 1 (row E: the shared-gate weight).
+template <int MH, bool EXACT>
+__device__ __forceinline__ void task_router(const DecodeParams& p, int t, int lane, uint32_t tag) {
   const int n_lrows = p.logits_in ? 0 : p.E;
   const int n_rows = n_lrows + (p.sh_gate ? 1 : 0);
-  const int row = t * 4 + wid;
-  if (row < n_rows) {
-    XFrag<MH> xf;
-    load_xfrag<MH>(xf, p.x, p.H, lane);
-    const uint16_t* rp[1] = {row < n_lrows ? p.router_w + (size_t)row * p.H : p.sh_gate_w};
-    float d[1];
-    wave_dots<MH, 1>(rp, xf, p.H, lane, d);
-    if (lane == 0) st64c(p.lg64 + (row < n_lrows ? row : p.E), tag64(__float_as_uint(d[0])));
+  const int r0 = t * kRouterRows;
+  if (r0 >= n_rows) return;
+  XPack<MH> xf;
+  load_xpack<MH, EXACT>(xf, p.x, p.H, lane);
+  const uint16_t* rp[kRouterRows];
+#pragma unroll
+  for (int r = 0; r < kRouterRows; ++r) {
+    const int row = min(r0 + r, n_rows - 1);
+    rp[r] = row < n_lrows ? p.router_w + (size_t)row * p.H : p.sh_gate_w;
+  }
+  float d[kRouterRows];
+  wave_dots_p<MH, kRouterRows, EXACT>(rp, xf, p.H, lane, d);
+  if (lane < kRouterRows && r0 + lane < n_rows) {
+    float v = d[0];
+#pragma unroll
+    for (int r = 1; r < kRouterRows; ++r) v = lane == r ? d[r] : v;
+    const int row = r0 + lane;
+    st64c(p.lg64 + (row < n_lrows ? row : p.E), tagged(tag, __float_as_uint(v)));
   }
 }
 
-// Zero the tagged logits, activations and routing of this call (the per-slot down
-// words are cleared by the combines that consume them).
-__device__ __forceinline__ void reset_graph(const DecodeParams& p) {
-  const int n = (p.E + 1) + (p.k * p.I + p.Is) / 2;
-  for (int i = threadIdx.x; i < n; i += 256) st64c(p.lg64 + i, 0ull);
-  const int rw = kRwW + p.k;   // route words in use per replica line
-  for (int i = threadIdx.x; i < kRouteReplicas * rw; i += 256) st32c(line(p, kLnRoute + i / rw) + i % rw, 0u);
-  if (threadIdx.x == 0) st32c(line(p, kLnCombined), 0u);
-}
-
-__device__ __forceinline__ uint64_t pack_pair_tagged(float a, float b) {
-  return tag64((uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16));
-}
-
-// A D(k-1) wave: combine rows h0..h0+7 from every slot's tagged down results (its
-// own in registers) and write the output.  One poll round covers everything: lane l
-// fetches one word -- l < k: slot ids, k <= l < 2k: weights, l == 2k: shared gate,
-// then 4 down pairs per earlier slot and 4 shared pairs -- the wave votes, and the
-// values are gathered with readlane.  Consumed down words are cleared.
+// A D(k-1) task: combine rows h0..h0+7 from every slot's tagged down results (its
+// own in registers) and write the output.  The routing comes from the wave's
+// cache.  Lane r < 8 owns row h0 + r: it reads the word holding that row for each
+// earlier slot and the shared expert (one batch of loads, clamped addresses),
+// then folds in router order, acc = bf16(acc + bf16(w_j * d_j)), and adds
+// bf16(gate * d_shared).
 __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, int h0, int lane,
-                                             const float (&d_last)[kFDownRowsPerWave], uint32_t* err) {
+                                             const float (&d_last)[kDownRows], uint32_t& rwc, uint32_t tag,
+                                             uint32_t* err) {
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
-  const int nq = 4 * (k - 1 + (has_sh ? 1 : 0));   // down pairs to fetch
-  const int q0 = 2 * k + 1;                         // first down-pair lane
-  const uint32_t* rt = route(p);
-  uint64_t* src = nullptr;
-  if (lane >= q0 && lane < q0 + nq) {
-    const int i = lane - q0, j = i / 4;             // j == k - 1 stands for the shared slot k
-    src = p.dq64 + ((size_t)(j == k - 1 ? k : j) * p.H + h0) / 2 + (i & 3);
+  if (!p.ids_in) {
+    const uint64_t need = ((1ull << k) - 1) | (has_sh ? 1ull << kRwGate : 0ull);
+    if (__ballot(rwc == kUnseenWord) & need) route_poll(p, lane, rwc, need, tag, err);
   }
-  uint32_t val = 0;
-  Backoff b;
+  const int r = lane & (kDownRows - 1);
+  // Word j holds this lane's row of slot j (j < k - 1) or, at j = k - 1, of the
+  // shared expert (slot k); words past that are never used.
+  uint32_t pr[kFusedMaxK];
+  Backoff<4> b;
   for (;;) {
+    uint64_t v[kFusedMaxK];
+#pragma unroll
+    for (int j = 0; j < kFusedMaxK; ++j) {
+      const int slot = j < k - 1 ? j : k;
+      v[j] = ld64c(p.dq64 + ((size_t)slot * p.H + h0 + r) / 2);
+    }
     bool ok = true;
-    if (lane < k) {
-      if (p.ids_in) {
-        val = (uint32_t)p.ids_in[lane];
-      } else {
-        const uint32_t v = ld32c(rt + kRwIds + lane);
-        ok = tagged32(v);
-        val = v & 0xFFFFu;
-      }
-    } else if (lane < 2 * k) {
-      if (p.w_in) {
-        val = p.w_in[lane - k];
-      } else {
-        const uint32_t v = ld32c(rt + kRwW + (lane - k));
-        ok = tagged32(v);
-        val = v & 0xFFFFu;
-      }
-    } else if (lane == 2 * k) {
-      if (has_sh) {
-        const uint32_t v = ld32c(rt + kRwGate);
-        ok = tagged32(v);
-        val = v & 0xFFFFu;
-      }
-    } else if (src) {
-      const uint64_t v = ld64c(src);
-      ok = tagged64(v);
-      val = (uint32_t)v;
+#pragma unroll
+    for (int j = 0; j < kFusedMaxK; ++j) {
+      const bool used = j < k - 1 || (j == k - 1 && has_sh);
+      ok &= !used || has_tag(v[j], tag);
+      pr[j] = (uint32_t)v[j];
     }
     if (__all(ok)) break;
     if (!b.step(err)) break;
   }
-  if (src) st64c(src, 0ull);
-  float acc[kFDownRowsPerWave] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // Lane r < 8 takes its own row of this slot (the row values are wave-uniform).
+  static_assert(kDownRows == 8, "one row per lane of lanes 0..7");
+  int rows[kDownRows];
+#pragma unroll
+  for (int i = 0; i < kDownRows; ++i) rows[i] = __float_as_int(d_last[i]);
+  const float own = __int_as_float(spread8(rows));
+  float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < kFusedMaxK; ++j) {
-    if (j >= k) continue;
-    const int e = j == k - 1 ? e_last : __builtin_amdgcn_readlane((int)val, j);
-    if (e < 0 || e >= p.E) continue;
-    const float wj = bf16_to_f32((uint16_t)__builtin_amdgcn_readlane((int)val, k + j));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float d0 = d_last[2 * q], d1 = d_last[2 * q + 1];
-      if (j != k - 1) {
-        const uint32_t pr = (uint32_t)__builtin_amdgcn_readlane((int)val, q0 + 4 * j + q);
-        d0 = bf16_lo(pr);
-        d1 = bf16_hi(pr);
-      }
-      acc[2 * q] = rbf16(acc[2 * q] + rbf16(wj * d0));
-      acc[2 * q + 1] = rbf16(acc[2 * q + 1] + rbf16(wj * d1));
-    }
+    if (j >= k) break;
+    const uint32_t rw = (uint32_t)__builtin_amdgcn_readlane((int)rwc, j);
+    const int e = j == k - 1 ? e_last : (int)(rw & 0xFFFFu);
+    if (e < 0 || e >= p.E || rw == kUnseenWord) continue;
+    const float wj = bf16_to_f32((uint16_t)(rw >> 16));
+    const float d = j == k - 1 ? own : ((r & 1) ? bf16_hi(pr[j]) : bf16_lo(pr[j]));
+    acc = rbf16(acc + rbf16(wj * d));
   }
   if (has_sh) {
-    const float g = bf16_to_f32((uint16_t)__builtin_amdgcn_readlane((int)val, 2 * k));
+    const float g = bf16_to_f32((uint16_t)__builtin_amdgcn_readlane((int)rwc, kRwGate));
+    uint32_t ps = pr[0];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t pr = (uint32_t)__builtin_amdgcn_readlane((int)val, q0 + 4 * (k - 1) + q);
-      acc[2 * q] = rbf16(acc[2 * q] + rbf16(g * bf16_lo(pr)));
-      acc[2 * q + 1] = rbf16(acc[2 * q + 1] + rbf16(g * bf16_hi(pr)));
-    }
+    for (int j = 1; j < kFusedMaxK; ++j) ps = j == k - 1 ? pr[j] : ps;
+    acc = rbf16(acc + rbf16(g * ((r & 1) ? bf16_hi(ps) : bf16_lo(ps))));
   }
-  if (lane == 0) {
-    uint32_t* o = reinterpret_cast<uint32_t*>(p.out + h0);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      o[q] = (uint32_t)f32_to_bf16(acc[2 * q]) | ((uint32_t)f32_to_bf16(acc[2 * q + 1]) << 16);
-  }
+  if (lane < kDownRows) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
 struct TaskRef {
   int type, slot, idx;
 };
 
+// Task t of the list R, K, then per slot j: Gj, D(j - kDownLag) once j >= kDownLag,
+// S after G(sh_after) and SD after G(sd_after); then the remaining D.  Pure arithmetic on values
+// held in scalar registers: a lookup table in kernel-argument memory costs a
+// memory round trip per step.
 __device__ __forceinline__ TaskRef decode_task(const DecodeParams& p, int t) {
   if (t < p.n_r) return {kTR, 0, t};
   t -= p.n_r;
@@ -424,12 +454,7 @@ __device__ __forceinline__ TaskRef decode_task(const DecodeParams& p, int t) {
     if (t == 0) return {kTK, 0, 0};
     t -= 1;
   }
-  if (t < p.n_s) return {kTS, 0, t};
-  t -= p.n_s;
-  if (p.sh_gate) {
-    if (t < p.n_rb) return {kTSD, p.k, t};
-    t -= p.n_rb;
-  }
+  const int n_sd = p.sh_gate ? p.n_rb : 0;
   for (int j = 0; j < p.k; ++j) {
     if (t < p.n_g) return {kTG, j, t};
     t -= p.n_g;
@@ -437,116 +462,154 @@ __device__ __forceinline__ TaskRef decode_task(const DecodeParams& p, int t) {
       if (t < p.n_rb) return {kTD, j - kDownLag, t};
       t -= p.n_rb;
     }
+    if (j == p.sh_after) {
+      if (t < p.n_s) return {kTS, 0, t};
+      t -= p.n_s;
+    }
+    if (j == p.sd_after) {
+      if (t < n_sd) return {kTSD, p.k, t};
+      t -= n_sd;
+    }
   }
   const int first = p.k > kDownLag ? p.k - kDownLag : 0;
   return {kTD, first + t / p.n_rb, t % p.n_rb};
 }
 
-template <int MH, int MI>
+// The call is over (every queue drained): advance the epoch.  At the wrap the hand-off area is zeroed first, so tags
+// restart at 1 with no stale match.
+__device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag, int lane) {
+  const bool wrap = tag == 0xFFFFFFFFu;
+  if (wrap) {
+    uint64_t* w = reinterpret_cast<uint64_t*>(p.handoff);
+    for (size_t i = lane; i < p.handoff_words; i += 64) st64c(w + i, 0ull);
+    for (int i = lane; i < kRouteReplicas * kLine; i += 64) st32c(line(p, kLnRoute) + i, 0u);
+  }
+  const uint32_t epoch = wrap ? 0u : tag;
+  if (lane < kQueues) st32c(line(p, kLnQueue + lane) + kQueueEpochWord, epoch);
+  if (lane == 0) {
+    st32c(line(p, kLnQueuesDone), 0u);
+    st32c(line(p, kLnEpoch), epoch);
+  }
+}
+
+template <int MH, int MI, bool EXACT>
 __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
-  __shared__ int s_flag, s_e, s_task;
-  __shared__ int s_id[kFusedMaxK];
-  __shared__ float s_lw[kFusedMaxK];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint32_t* err = p.status + kStatusError;
-  const int q = (int)(blockIdx.x % kQueues);
+  const int q = (int)(blockIdx.x % 8) * kWaves + wid;
   uint32_t* queue = line(p, kLnQueue + q);
-  uint32_t next = 0;
-  if (threadIdx.x == 0) next = atomicAdd(queue, 1u);
-  for (;;) {
-    if (threadIdx.x == 0) s_task = q + kQueues * (int)next;
-    __syncthreads();
-    const int t = s_task;
-    __syncthreads();
+  const uint32_t users = (gridDim.x - (uint32_t)(q / kWaves) + 7u) / 8u;
+  const uint32_t rank = blockIdx.x / 8u;
+  // Every lane loads the epoch (one transaction); kept per lane, the value is
+  // first waited for where a task stores or polls.
+  const uint32_t tag = ld32c(queue + kQueueEpochWord) + 1u;
+  uint32_t rwc = kUnseenWord;   // this wave's routing cache
+  if (p.ids_in && lane < p.k) {
+    // Caller-supplied routing (ids outside [0, E) are skipped; E is the sentinel).
+    const int64_t e = p.ids_in[lane];
+    rwc = ((uint32_t)p.w_in[lane] << 16) | (e >= 0 && e < p.E ? (uint32_t)e : 0xFFFFu);
+    if ((e < 0 || e > p.E) && blockIdx.x == 0 && wid == 0) atomicOr(err, kErrExpertId);
+  }
+  for (uint32_t i = 0;; ++i) {
+    // Tickets rank, rank + users, ... of queue q: no atomic between tasks (a wait
+    // on a draw would also wait for this wave's stores, which gfx9 counts in vmcnt).
+    const int t = q + kQueues * (int)(rank + users * i);
     if (t >= p.n_tasks) break;
-    if (threadIdx.x == 0) next = atomicAdd(queue, 1u);      // draw the next task while this one runs
     const TaskRef tk = decode_task(p, t);
     if (tk.type == kTR) {
-      task_router<MH>(p, tk.idx, lane, wid, err);
+      task_router<MH, EXACT>(p, tk.idx, lane, tag);
     } else if (tk.type == kTK) {
-      if (wid == 0) {
-        if (p.E <= 256)
-          resolve_routing<4>(p, lane, err, s_id, s_lw);
-        else
-          resolve_routing<16>(p, lane, err, s_id, s_lw);
-      }
+      if (p.E <= 256)
+        resolve_routing<4>(p, lane, tag, err);
+      else
+        resolve_routing<16>(p, lane, tag, err);
     } else if (tk.type == kTS || tk.type == kTG) {
       // Gate/up pairs: the shared expert (S) or routed slot j (G); one call site.
       const bool shared = tk.type == kTS;
-      const int e = shared ? 0 : block_slot_expert(p, tk.slot, &s_e, err);
+      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err);
       const int n_rows = shared ? p.Is : p.I;
-      const int i0 = tk.idx * kFPairsPerTask + wid * kFPairsPerWave;
-      if (e >= 0 && i0 < n_rows) {
-        const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(p.table[2 * e]);
+      const int i0 = tk.idx * kPairs;
+      if (e >= 0) {
+        const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
         const uint16_t* g = shared ? p.sh_gate : gu;
         const uint16_t* u = shared ? p.sh_up : gu + (size_t)p.I * p.H;
-        up_pairs<MH>(g, u, i0, n_rows, p.H, p.x, lane,
-                     p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2));
+        up_pairs<MH, EXACT>(g, u, i0, n_rows, p.H, p.x, lane,
+                            p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag);
       }
     } else {
-      // Down rows: the shared expert (SD, kept for the last fold) or routed slot j (D, folded).
+      // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
-      const int e = shared ? 0 : block_slot_expert(p, tk.slot, &s_e, err);
-      const int h0 = tk.idx * kFDownRowsPerTask + wid * kFDownRowsPerWave;
-      float d[kFDownRowsPerWave] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (e >= 0 && h0 < p.H) {
-        const uint16_t* w = shared ? p.sh_down : reinterpret_cast<const uint16_t*>(p.table[2 * e + 1]);
+      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err);
+      const int h0 = tk.idx * kDownRows;
+      float d[kDownRows] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (e >= 0) {
+        const uint16_t* w = shared ? p.sh_down : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e + 1));
         const uint64_t* a = p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2);
-        down_dots<MI>(w, a, shared ? p.Is : p.I, p.H, h0, lane, d, err);
+        down_dots<MI, EXACT>(w, a, p, shared ? p.Is : p.I, h0, lane, d, tag, err);
       }
-      const bool last = !shared && tk.slot == p.k - 1;
-      if (!last) {
+      if (shared || tk.slot != p.k - 1) {
         // Publish this slot's rows (a skipped slot publishes zeros the combine ignores).
-        if (lane == 0 && h0 < p.H) {
-          uint64_t* dst = p.dq64 + ((size_t)(shared ? p.k : tk.slot) * p.H + h0) / 2;
+        // Lane q < 4 publishes rows 2q, 2q + 1 (the row values are wave-uniform).
+        int pairs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-          for (int q = 0; q < 4; ++q) st64c(dst + q, pack_pair_tagged(d[2 * q], d[2 * q + 1]));
-        }
+        for (int q2 = 0; q2 < kDownRows / 2; ++q2)
+          pairs[q2] = (int)((uint32_t)f32_to_bf16(d[2 * q2]) | ((uint32_t)f32_to_bf16(d[2 * q2 + 1]) << 16));
+        const int pair = spread8(pairs);
+        if (lane < kDownRows / 2)
+          st64c(p.dq64 + ((size_t)(shared ? p.k : tk.slot) * p.H + h0) / 2 + lane, tagged(tag, (uint32_t)pair));
       } else {
-        if (h0 < p.H) combine_rows(p, e, h0, lane, d, err);
-        // Every combine of the call done: clear the hand-off words for the next call.
-        wait_stores();
-        __syncthreads();
-        if (threadIdx.x == 0)
-          s_flag = __hip_atomic_fetch_add(line(p, kLnCombined), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (uint32_t)p.n_rb - 1u;
-        __syncthreads();
-        if (s_flag) reset_graph(p);
+        combine_rows(p, e, h0, lane, d, rwc, tag, err);
       }
     }
   }
-  // The last block to leave queue q re-zeroes its lines (every draw from it is done).
-  if (threadIdx.x == 0) {
-    const uint32_t users = (gridDim.x - (uint32_t)q + kQueues - 1) / kQueues;
-    const uint32_t prev =
-        __hip_atomic_fetch_add(line(p, kLnQueueExit + q), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == users - 1u) {
-      st32c(queue, 0u);
+  // The last wave to leave queue q re-zeroes its exit count; the last queue to
+  // drain ends the call.
+  uint32_t fin = 0;
+  if (lane == 0) {
+    if (add32c(line(p, kLnQueueExit + q), 1u) == users - 1u) {
       st32c(line(p, kLnQueueExit + q), 0u);
+      fin = add32c(line(p, kLnQueuesDone), 1u) == (uint32_t)kQueues - 1u;
     }
   }
+  if (__builtin_amdgcn_readfirstlane(fin)) finish_call(p, tag, lane);
 }
 
 // ---------------------------------------------------------------- launch
 typedef void (*FusedKernel)(DecodeParams);
 
-static FusedKernel pick_fused(int ncH, int ncI) {
+// Exact-fit variants (H = 512 MH, I = Is = 512 MI) for the common layer widths;
+// masked variants cover the rest up to H = 4096, I = Is = 2048.
+static FusedKernel pick_fused(int H, int I, int Is) {
+  if (H % 512 == 0 && I % 512 == 0 && (Is == 0 || Is == I)) {
+    switch ((H / 512) * 10 + I / 512) {
+      case 21: return k_decode_fused<2, 1, true>;
+      case 22: return k_decode_fused<2, 2, true>;
+      case 42: return k_decode_fused<4, 2, true>;
+      case 52: return k_decode_fused<5, 2, true>;
+      case 62: return k_decode_fused<6, 2, true>;
+      case 84: return k_decode_fused<8, 4, true>;
+    }
+  }
+  const int inter = I > Is ? I : Is;
+  const int ncH = (H + 511) / 512, ncI = (inter + 511) / 512;
   const int mh = ncH <= 2 ? 2 : ncH <= 4 ? 4 : ncH <= 6 ? 6 : ncH <= 8 ? 8 : 0;
   const int mi = ncI <= 2 ? 2 : ncI <= 4 ? 4 : 0;
   switch (mh * 10 + mi) {
-    case 22: return k_decode_fused<2, 2>;
-    case 24: return k_decode_fused<2, 4>;
-    case 42: return k_decode_fused<4, 2>;
-    case 44: return k_decode_fused<4, 4>;
-    case 62: return k_decode_fused<6, 2>;
-    case 64: return k_decode_fused<6, 4>;
-    case 82: return k_decode_fused<8, 2>;
-    case 84: return k_decode_fused<8, 4>;
+    case 22: return k_decode_fused<2, 2, false>;
+    case 24: return k_decode_fused<2, 4, false>;
+    case 42: return k_decode_fused<4, 2, false>;
+    case 44: return k_decode_fused<4, 4, false>;
+    case 62: return k_decode_fused<6, 2, false>;
+    case 64: return k_decode_fused<6, 4, false>;
+    case 82: return k_decode_fused<8, 2, false>;
+    case 84: return k_decode_fused<8, 4, false>;
   }
   return nullptr;
 }
 
-// Blocks of a kernel that can be resident at once on the current device (cached).
+// Blocks of a kernel to launch on the current device (cached): every one resident
+// at once, at most kBlocksPerCU per CU.
 static int resident_blocks(FusedKernel k) {
   static std::mutex mu;
   static struct {
@@ -564,27 +627,31 @@ static int resident_blocks(FusedKernel k) {
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k), 256, 0) != hipSuccess)
     return 0;
-  const int n = cu * (occ > 0 ? occ : 1);
+  const int n = cu * (occ < 1 ? 1 : occ < kBlocksPerCU ? occ : kBlocksPerCU);
   if (used < 64) cache[used++] = {dev, k, n};
   return n;
 }
 
 int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   const bool has_sh = p.sh_gate != nullptr;
-  const int ncH = (p.H + 511) / 512;
-  const int ncI = ((p.I > p.Is ? p.I : p.Is) + 511) / 512;
-  FusedKernel k = pick_fused(ncH, ncI);
-  p.n_rb = (p.H + kFDownRowsPerTask - 1) / kFDownRowsPerTask;
-  if (!k || p.n_rb > kMaxRowBlocks || p.k > kFusedMaxK || (has_sh && !run_router) || (p.I & 1) || (p.Is & 1))
+  FusedKernel k = pick_fused(p.H, p.I, p.Is);
+  if (!k || p.k > kFusedMaxK || (has_sh && !run_router) || (p.I & 1) || (p.Is & 1) || (p.H % kDownRows))
     return TMOE_ERR_SHAPE;
   const int n_rows = (p.logits_in ? 0 : p.E) + (has_sh ? 1 : 0);
-  p.n_r = run_router ? (n_rows > 0 ? (n_rows + 3) / 4 : 1) : 0;
-  p.n_s = has_sh ? (p.Is + kFPairsPerTask - 1) / kFPairsPerTask : 0;
-  p.n_g = (p.I + kFPairsPerTask - 1) / kFPairsPerTask;
+  p.n_r = run_router ? (n_rows > 0 ? (n_rows + kRouterRows - 1) / kRouterRows : 1) : 0;
+  p.n_s = has_sh ? (p.Is + kPairs - 1) / kPairs : 0;
+  p.n_g = (p.I + kPairs - 1) / kPairs;
+  p.n_rb = p.H / kDownRows;
+  // While the routing resolves only the router rows load: any request issued
+  // behind a full memory queue waits microseconds, and every routing step is one.
+  p.sh_after = p.k - 1 < kSharedAfter ? p.k - 1 : kSharedAfter;
+  p.sd_after = p.k - 1 < p.sh_after + kDownLag ? p.k - 1 : p.sh_after + kDownLag;
   p.n_tasks = p.n_r + (p.n_r ? 1 : 0) + p.n_s + (has_sh ? p.n_rb : 0) + p.k * (p.n_g + p.n_rb);
   int grid = resident_blocks(k);
   if (grid <= 0) return TMOE_ERR_HIP;
-  if (grid > p.n_tasks) grid = p.n_tasks;
+  const int need = (p.n_tasks + kWaves - 1) / kWaves;
+  if (grid > need) grid = need;
+  if (grid < 8) grid = 8;   // every queue needs a wave
   hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }

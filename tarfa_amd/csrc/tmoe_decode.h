@@ -33,12 +33,14 @@ struct DecodeParams {
   uint16_t* sact_ws;          // [Is]
   uint16_t* sh_ws;            // [H]
   // fused task graph (tmoe_decode_fused)
-  uint16_t* dbuf;             // [(k + 1), H] per-slot down outputs (slot k = shared expert, before its gate)
   uint32_t* sync;             // task-graph lines
   uint64_t* lg64;             // [E + 1] tagged fp32 logits (index E: shared-gate logit)
   uint64_t* act64;            // [k * I / 2] tagged bf16 activation pairs, then [Is / 2] shared
   uint64_t* dq64;             // [(k + 1) * H / 2] tagged per-slot down pairs (slot k: shared, before its gate)
+  void* handoff;              // workspace past the sync lines: zeroed when the epoch wraps
+  size_t handoff_words;       // its size in uint64
   int n_r, n_s, n_g, n_rb, n_tasks;   // task counts: router, shared up, gate/up per slot, row blocks; total
+  int sh_after, sd_after;     // shared gate/up (S) and shared down (SD) follow these slots' gate/up tasks
 };
 
 }  // namespace tmoe

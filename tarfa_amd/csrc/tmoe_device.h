@@ -24,12 +24,13 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.  Written as a
+// select, not a branch: it runs per lane inside hot loops.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u >> 16) | 0x40u;
+  return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? quiet : rounded);
 }
 // Round an fp32 value to the nearest bf16 value, kept in fp32.
 __device__ __forceinline__ float rbf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -66,6 +67,20 @@ __device__ __forceinline__ float dot8bb(const u32x4 w, const u32x4 a, float acc)
   acc = fmaf(bf16_hi(w.z), bf16_hi(a.z), acc);
   acc = fmaf(bf16_lo(w.w), bf16_lo(a.w), acc);
   acc = fmaf(bf16_hi(w.w), bf16_hi(a.w), acc);
+  return acc;
+}
+
+// Dot of 8 bf16 weights with 8 bf16 activations, both packed in 4 dwords:
+// v_dot2c_f32_bf16 (exact bf16 products, fp32 accumulation), pairs in column order.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2bf(uint32_t w, uint32_t a, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, a), acc, false);
+}
+__device__ __forceinline__ float dot8p(const u32x4 w, const u32x4 a, float acc) {
+  acc = dot2bf(w.x, a.x, acc);
+  acc = dot2bf(w.y, a.y, acc);
+  acc = dot2bf(w.z, a.z, acc);
+  acc = dot2bf(w.w, a.w, acc);
   return acc;
 }
 
@@ -111,6 +126,35 @@ __device__ __forceinline__ int wave_min_int(int v) {
   int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
   int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
   return min(min(a, b), min(c, d));
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppXor1, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppXor2, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppHalfMirror, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppMirror, 0xF, 0xF, true);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+}
+
+// Lane L of v takes the wave-uniform value s (v_writelane_b32).
+template <int L>
+__device__ __forceinline__ int set_lane(int v, int s) {
+  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(s), "n"(L));
+  return v;
+}
+// Lanes 0..7 take vals[0..7] (wave-uniform values).
+__device__ __forceinline__ int spread8(const int (&vals)[8]) {
+  int v = 0;
+  v = set_lane<0>(v, vals[0]);
+  v = set_lane<1>(v, vals[1]);
+  v = set_lane<2>(v, vals[2]);
+  v = set_lane<3>(v, vals[3]);
+  v = set_lane<4>(v, vals[4]);
+  v = set_lane<5>(v, vals[5]);
+  v = set_lane<6>(v, vals[6]);
+  v = set_lane<7>(v, vals[7]);
+  return v;
 }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }

@@ -52,6 +52,44 @@ __device__ __forceinline__ void wave_dots(const uint16_t* const (&rows)[R], cons
   }
 }
 
+// The same vector kept packed (bf16 pairs): lane l holds columns c*512 + 8l .. +7
+// of chunk c as 4 dwords.  EXACT: K == MAXC * 512, so no column is masked.
+template <int MAXC>
+struct XPack {
+  u32x4 v[MAXC];
+};
+
+template <int MAXC, bool EXACT>
+__device__ __forceinline__ void load_xpack(XPack<MAXC>& f, const uint16_t* __restrict__ x, int K, int lane) {
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int col = c * 512 + lane * 8;
+    f.v[c] = (EXACT || col < K) ? ld16(x + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// Dots of R weight rows with a packed fragment (v_dot2 bf16, fp32 accumulation);
+// all R x MAXC 16-byte loads are issued before any arithmetic.  Every lane gets the sums.
+template <int MAXC, int R, bool EXACT>
+__device__ __forceinline__ void wave_dots_p(const uint16_t* const (&rows)[R], const XPack<MAXC>& xf, int K, int lane,
+                                            float (&out)[R]) {
+  u32x4 w[R][MAXC];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int col = c * 512 + lane * 8;
+      w[r][c] = (EXACT || col < K) ? ld_stream(rows[r] + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) acc = dot8p(w[r][c], xf.v[c], acc);
+    out[r] = wave_sum(acc);
+  }
+}
+
 // Top-k of E fp32 logits by one wave (lane l owns experts l + 64 i, i < MAXEPL).
 // Order: logit descending, ties to the lower expert index.  Probabilities are
 // softmax in fp32 (max-subtracted), renormalised over the k selected in router

@@ -16,27 +16,28 @@ enum ErrorBit { kErrExpertId = 1u, kErrTimeout = 2u };
 
 // Synchronisation lines of the fused decode task graph.  Every counter owns a
 // 256-byte line (64 uint32): atomics on one hot line serialise at ~11 ns each.
-// All are zero between calls: the last row-block combine of a call re-zeroes the
-// task-graph lines, and the last block to leave a queue re-zeroes that queue's lines.
+// Counters are zero between calls (the last wave to leave a queue re-zeroes its
+// exit count).  Hand-off words
+// (logits, routing, activations, per-slot down results) are 64-bit {payload,
+// tag}: the tag is the call's epoch, so words left by earlier calls never match
+// and nothing is cleared between calls.
 constexpr int kLine = 64;                 // uint32 per line
-constexpr int kMaxSlots = 16;             // top-k
-constexpr int kMaxRowBlocks = 128;        // H / 32
 constexpr int kRouteReplicas = 32;        // routing published to this many lines
-// Tagged hand-off words of the fused decode: a value and its valid tag travel in
-// one coherent store, so a consumer polls the data itself.  Zero = not written.
-constexpr uint32_t kTag16 = 0xA5A5u;      // high half of a 32-bit routing word (payload: low 16 bits)
-constexpr uint32_t kTag32 = 0x5A5A5A5Au;  // high word of a 64-bit logit / activation / shared-down word
-constexpr int kQueues = 8;                // task queues (one per XCD-sized group of blocks)
+constexpr int kQueues = 32;               // task queues: 4 waves x 8 XCD-sized groups of blocks
 enum SyncLine {
-  kLnCombined = 0,                        // row blocks combined
-  kLnQueue = 1,                           // [kQueues] next draw index per queue
-  kLnQueueExit = kLnQueue + kQueues,      // [kQueues] blocks that left each queue
-  kLnRowDone = kLnQueueExit + kQueues,    // [kMaxRowBlocks] down tasks finished per row block
-  kLnRoute = kLnRowDone + kMaxRowBlocks,  // [kRouteReplicas]: tagged {gate, ids[16], w[16]}
+  kLnEpoch = 0,                           // word 0: epoch of the next call (tag = epoch + 1)
+  kLnQueuesDone = 1,                      // queues fully drained this call
+  kLnQueue = 2,                           // [kQueues] word kQueueEpochWord: epoch copy for the queue's waves
+  kLnQueueExit = kLnQueue + kQueues,      // [kQueues] waves that left each queue
+  kLnRoute = kLnQueueExit + kQueues,      // [kRouteReplicas] u64 {slot[8], gate}
   kSyncLines = kLnRoute + kRouteReplicas,
 };
-// Word offsets inside a route replica line.
-enum RouteWord { kRwGate = 0, kRwIds = 1, kRwW = 1 + kMaxSlots };
+// Each queue line also carries a copy of the epoch, read by that queue's waves
+// (coherent loads of one line serialise, so 2048 waves must not share one word).
+constexpr int kQueueEpochWord = 16;
+// u64 words of a route replica line: slot j = {tag, bf16 weight << 16 | expert id},
+// then the shared-expert gate {tag, bf16 gate}.
+enum RouteWord { kRwSlot = 0, kRwGate = 8, kRouteWords = 9 };
 
 struct Ws {
   size_t status;   // uint32[kStatusSlots]
@@ -52,7 +53,6 @@ struct Ws {
   size_t inv;      // int32[T * k]
   size_t scratch;  // int32[E + 64]      dispatch counters
   size_t ch;       // bf16[T * k * H]    weighted per-assignment expert outputs (T > 1)
-  size_t dbuf;     // bf16[(k + 1) * H]  per-expert down outputs of the fused decode (T == 1)
   size_t tagged;   // u64[(E + 1) + (k * I + Is) / 2 + (k + 1) * H / 2]  tagged logits, activation
                    // pairs, per-slot down pairs (slot k = shared expert)
   size_t total;
@@ -79,7 +79,6 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.inv = take(sizeof(int32_t) * t * (size_t)k);
   w.scratch = take(sizeof(int32_t) * (size_t)(E + 64));
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
-  w.dbuf = take(2 * (size_t)(k + 1) * (size_t)H);
   w.tagged = take(8 * ((size_t)(E + 1) + ((size_t)k * I + (size_t)Is) / 2 + (size_t)(k + 1) * H / 2));
   w.total = o;
   return w;

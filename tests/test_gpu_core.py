@@ -125,6 +125,66 @@ def test_decode_sentinel_and_invalid_ids(gpu):
         ws.status()
 
 
+# Fused-decode workspace layout: a status block (64 uint32), then 256-byte lines;
+# line 0 word 0 holds the epoch, lines 2..33 are the task queues, each with a copy
+# of the epoch in word 16 (read by that queue's waves).
+EPOCH_BYTE = 256
+EPOCH_COPIES = [256 + (2 + q) * 256 + 16 * 4 for q in range(32)]
+
+
+def _epoch(ws):
+    vals = [int(ws.buf[o:o + 4].cpu().view(torch.int32).numpy().view(np.uint32)[0])
+            for o in [EPOCH_BYTE] + EPOCH_COPIES]
+    assert len(set(vals)) == 1, f"epoch copies disagree: {sorted(set(vals))}"
+    return vals[0]
+
+
+def _set_epoch(ws, value):
+    b = torch.tensor(list(value.to_bytes(4, "little")), dtype=torch.uint8, device=ws.buf.device)
+    for o in [EPOCH_BYTE] + EPOCH_COPIES:
+        ws.buf[o:o + 4] = b
+
+
+def test_decode_workspace_reuse_and_epoch_wrap(gpu):
+    """Back-to-back decode calls on one workspace, across the 2^32 epoch wrap.
+
+    Hand-off words carry the call's epoch, so each call must ignore every word an
+    earlier call left behind; each output is checked against the oracle.
+    """
+    shape = MoEShape(1024, 32, 512, 8, 512)
+    layer = seeded.make_layer(shape, 21, device=gpu)
+    ws = Workspace(shape, gpu)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    xs = seeded.make_tokens(shape, 21, 9, device=gpu)
+    shared = [f32(t) for t in layer.shared]
+
+    def one(r):
+        x = xs[r:r + 1]
+        out, ids, w = tm.moe_block(shape, x, table, ws, router_w=layer.router_w, shared=layer.shared)
+        torch.cuda.synchronize()
+        xf = f32(x)
+        lg = moe.router_logits(xf, f32(layer.router_w))
+        ids_ref, w_ref = _check_routing(ids.cpu().numpy(), f32(w), lg, shape.top_k, f"reuse call {r}")
+        gu, dn = expert_dicts(layer.gate_up, layer.down, ids_ref)
+        ref = moe.add_bf16(moe.experts_decode(xf[0], ids_ref[0], w_ref[0], gu, dn, shape.num_experts),
+                           moe.shared_expert(xf[0], *shared))
+        assert_close_bf16(f32(out)[0], ref, f"reuse call {r}")
+
+    assert _epoch(ws) == 0
+    for r in range(4):
+        one(r)
+        assert _epoch(ws) == r + 1
+    _set_epoch(ws, 0xFFFFFFFD)
+    one(4)
+    assert _epoch(ws) == 0xFFFFFFFE
+    one(5)
+    assert _epoch(ws) == 0                    # tag 0xFFFFFFFF: the hand-off area is zeroed, epoch restarts
+    one(6)
+    assert _epoch(ws) == 1
+    one(7)
+    ws.status()
+
+
 @pytest.mark.parametrize("T,E,k", [(4096, 256, 8), (5, 32, 8), (1000, 16, 1), (300, 4, 2)])
 def test_dispatch_bit_exact(gpu, T, E, k):
     g = np.random.default_rng(T + E)
