@@ -32,8 +32,8 @@
 //   - A down task reads its activations with plain loads issued together with its
 //     weight rows (queued kDownLag slots after its gate/up tasks, the activations
 //     are normally complete); stale words are re-polled with coherent loads.
-//   - Each wave caches the routing it has seen (lane l: slot l's expert), so only
-//     its first task of a slot waits for the id.
+//   - Each wave caches the routing it has seen; a block keeps a copy in LDS and one
+//     of its waves at a time polls memory, so every block asks memory once.
 //   - Queue q (of 32) is served by wave q % 4 of the blocks b with b % 8 == q / 4
 //     (one XCD) and holds tasks q, q + 32, ...; the wave of rank r = b / 8 among
 //     its queue's `users` takes tickets r, r + users, r + 2 users, ...  Each wave
@@ -57,7 +57,7 @@ constexpr int kRouterRows = 4;         // router rows per R task
 constexpr int kPairs = 2;              // gate/up row pairs per G / S task (4 rows of K = H in flight)
 constexpr int kDownRows = 8;           // down rows per D / SD task (8 rows of K = I in flight)
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
-constexpr int kDownLag = 3;            // Dj is queued after G(j + kDownLag)
+constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
 constexpr int kBlocksPerCU = 2;        // resident blocks per CU (bounds the bytes in flight per XCD)
 constexpr uint32_t kSpinLimit = 1u << 20;   // polls, each >= 64 cycles apart: never reached by a healthy graph
@@ -159,39 +159,71 @@ __device__ __forceinline__ void load_acts(XPack<MAXC>& f, const uint64_t* w, int
   }
 }
 
-__device__ __forceinline__ const uint64_t* route(const DecodeParams& p) {
-  return line64(p, kLnRoute + (int)(blockIdx.x % kRouteReplicas));
+__device__ __forceinline__ uint64_t* route_line(const DecodeParams& p, int r) {
+  return line64(p, kLnRoute + r * kRouteStride);
 }
 
-// The wave's routing cache: lane l < k holds slot l's route word {weight, id},
-// lane kRwGate the shared gate, once seen (kUnseenWord before).  A poll refreshes
-// every missing word at once until the lanes in `need` are all seen.
+// Routing as seen by one block: the route words (lane layout of RouteWord) and a
+// mask of those known; one wave at a time polls memory for the block.
+struct RouteLds {
+  uint32_t word[kRouteWords];
+  uint32_t valid;
+  uint32_t poller;
+};
+
+// The wave's routing cache `rwc` (lane l < kRouteWords holds route word l once
+// seen, kUnseenWord before) is completed until every lane in `need` is seen:
+// from the block's copy in LDS, else by becoming the block's poller.
 constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
 
-__device__ __forceinline__ void route_poll(const DecodeParams& p, int lane, uint32_t& rwc, uint64_t need, uint32_t tag,
-                                           uint32_t* err) {
-  const bool mine = lane < p.k || (lane == kRwGate && p.sh_gate != nullptr);
-  const uint64_t* rt = route(p);
+__device__ __forceinline__ void route_fetch(const DecodeParams& p, int lane, uint32_t& rwc, uint32_t need, uint32_t tag,
+                                         uint32_t* err, RouteLds& L) {
+  const uint64_t* rt = route_line(p, (int)(blockIdx.x % kRouteReplicas));
+  const bool has_sh = p.sh_gate != nullptr;
+  const bool used = lane < p.k || (lane >= kRwW && lane < kRwW + p.k) || (lane == kRwGate && has_sh);
   Backoff<16> b;
   for (;;) {
-    if (mine && rwc == kUnseenWord) {
-      const uint64_t w = ld64c(rt + lane);
-      if (has_tag(w, tag)) rwc = (uint32_t)w;
+    const uint32_t valid = __hip_atomic_load(&L.valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if ((valid & need) == need) {
+      if (lane < kRouteWords && ((valid >> lane) & 1u)) rwc = L.word[lane];
+      return;
     }
-    if (!(__ballot(rwc == kUnseenWord) & need)) return;
+    uint32_t got = 0;
+    if (lane == 0) got = atomicCAS(&L.poller, 0u, 1u) == 0u;
+    if (__builtin_amdgcn_readfirstlane(got)) {
+      // This wave polls the block's replica until the words in `need` are published.
+      for (;;) {
+        uint64_t w = 0;
+        if (used) w = ld64c(rt + lane);
+        const bool now = used && has_tag(w, tag);
+        const uint32_t nv = (uint32_t)__ballot(now);
+        if (now) L.word[lane] = (uint32_t)w;
+        __threadfence_block();
+        if (lane == 0) atomicOr(&L.valid, nv);
+        if ((nv & need) == need) break;
+        if (!b.step(err)) break;
+      }
+      if (lane == 0) atomicExch(&L.poller, 0u);
+      const uint32_t v2 = __hip_atomic_load(&L.valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (lane < kRouteWords && ((v2 >> lane) & 1u)) rwc = L.word[lane];
+      return;
+    }
     if (!b.step(err)) return;
   }
+}
+
+__device__ __forceinline__ void route_need(const DecodeParams& p, int lane, uint32_t& rwc, uint32_t need, uint32_t tag,
+                                           uint32_t* err, RouteLds& L) {
+  if ((uint32_t)__ballot(rwc == kUnseenWord) & need) route_fetch(p, lane, rwc, need, tag, err, L);
 }
 
 // Expert of slot j (wave-uniform) for this wave, or -1 for a skipped or invalid id
 // (caller-supplied routing is in the cache from the start).
 __device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, int lane, uint32_t& rwc, uint32_t tag,
-                                                uint32_t* err) {
-  if (!p.ids_in && (uint32_t)__builtin_amdgcn_readlane((int)rwc, j) == kUnseenWord)
-    route_poll(p, lane, rwc, 1ull << j, tag, err);
-  const uint32_t w = (uint32_t)__builtin_amdgcn_readlane((int)rwc, j);
-  const int e = (int)(w & 0xFFFFu);
-  return (w != kUnseenWord && e < p.E) ? e : -1;
+                                                uint32_t* err, RouteLds& L) {
+  if (!p.ids_in) route_need(p, lane, rwc, 1u << (kRwId + j), tag, err, L);
+  const uint32_t w = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwId + j);
+  return (w != kUnseenWord && (int)w < p.E) ? (int)w : -1;
 }
 
 // SwiGLU of gate/up row pairs [i0, i0 + 2): one tagged activation pair.
@@ -283,33 +315,60 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
       if (!b.step(err)) break;
     }
   }
-  // Selection rounds: logit descending, ties to the lower expert index.  Lane r
-  // keeps slot r; nothing is stored until the routing is complete (a store waits
-  // behind the streaming loads queued on this CU).
-  uint32_t sel = 0;
+  // Selection rounds: logit descending, ties to the lower expert index.  Each lane
+  // first sorts its MAXEPL logits (value descending, index ascending), so a round
+  // is one max over the lane heads, a ballot for the winner, and a pop.
+  float a[MAXEPL];
+  int ai[MAXEPL];
+#pragma unroll
+  for (int i = 0; i < MAXEPL; ++i) {
+    a[i] = lane + 64 * i < p.E ? v[i] : -INFINITY;
+    ai[i] = lane + 64 * i;
+  }
+#pragma unroll
+  for (int x = 0; x < MAXEPL; ++x)
+#pragma unroll
+    for (int y = MAXEPL - 1; y > x; --y) {
+      const bool sw = a[y] > a[y - 1];   // equal values keep the lower index (earlier) first
+      const float fa = sw ? a[y] : a[y - 1], fb = sw ? a[y - 1] : a[y];
+      const int ia = sw ? ai[y] : ai[y - 1], ib = sw ? ai[y - 1] : ai[y];
+      a[y - 1] = fa; a[y] = fb; ai[y - 1] = ia; ai[y] = ib;
+    }
   int my_id = p.E;          // lane r < k: slot r's expert and logit
   float my_lw = -INFINITY;
   float m = 0.f;            // the largest logit (slot 0)
 #pragma unroll 1
   for (int r = 0; r < p.k; ++r) {
-    float bv = -INFINITY;
-    int bi = INT_MAX;
-#pragma unroll
-    for (int i = 0; i < MAXEPL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < p.E && !((sel >> i) & 1u) && (bi == INT_MAX || v[i] > bv)) {
-        bv = v[i];
-        bi = e;
-      }
+    const float g = wave_max(a[0]);
+    const uint64_t cand = __ballot(a[0] == g && a[0] != -INFINITY);
+    int win;
+    if (__builtin_popcountll(cand) == 1) {
+      win = __builtin_amdgcn_readlane(ai[0], (int)__builtin_ctzll(cand));
+    } else {
+      // Equal logits in several lanes (or none left): lowest index among them.
+      win = wave_min_int(a[0] == g && a[0] != -INFINITY ? ai[0] : INT_MAX);
     }
-    const float g = wave_max(bv);
-    const int win = wave_min_int((bi != INT_MAX && bv == g) ? bi : INT_MAX);
-    if (win != INT_MAX && (win & 63) == lane) sel |= 1u << (win >> 6);
+    if (win != INT_MAX && (win & 63) == lane) {
+#pragma unroll
+      for (int i = 0; i + 1 < MAXEPL; ++i) {
+        a[i] = a[i + 1];
+        ai[i] = ai[i + 1];
+      }
+      a[MAXEPL - 1] = -INFINITY;
+    }
     if (lane == r) {
       my_id = win == INT_MAX ? p.E : win;
       my_lw = g;
     }
     if (r == 0) m = g;
+  }
+  // Publish the ids at once (the gate/up tasks need nothing else): lane l writes
+  // id word l % 8 of replica l / 8 (one store instruction per 8 replicas).
+#pragma unroll
+  for (int it = 0; it < kRouteReplicas / 8; ++it) {
+    const int slot = lane & 7;
+    const uint32_t id = (uint32_t)__builtin_amdgcn_ds_bpermute(slot * 4, my_id);
+    if (slot < p.k) st64c(route_line(p, it * 8 + (lane >> 3)) + kRwId + slot, tagged(tag, id));
   }
   // Softmax over all E in fp32 (max-subtracted), renormalised over the k
   // selected, rounded to bf16 -- one slot per lane.
@@ -323,19 +382,18 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
   const float psum = wave_sum(pr);   // all lanes active: a DPP reduction must not run divergent
   const float wr = (mine && my_id < p.E) ? rbf16(pr / psum) : 0.f;
   const uint32_t wb = f32_to_bf16(wr);
-  // Route words: lane r < k holds slot r's {weight, id}; lane kRwGate the gate.
-  uint32_t word = ((uint32_t)wb << 16) | (uint32_t)my_id;
-  if (lane == kRwGate) word = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
-  // Replica i of kRouteReplicas gets words 0 .. kRouteWords-1; lane l writes word
-  // (it * 64 + l) of the flattened replicas.
+  // Then the weights and the gate: lane l < 8 holds weight l, lane 8 the gate;
+  // word w (0..8) of replica r is written by flattened lane r * 9 + w.
+  uint32_t word = wb;
+  if (lane == 8) word = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
 #pragma unroll
-  for (int it = 0; it < (kRouteReplicas * kRouteWords + 63) / 64; ++it) {
+  for (int it = 0; it < (kRouteReplicas * 9 + 63) / 64; ++it) {
     const int f = it * 64 + lane;
-    const int rw = f % kRouteWords;
-    const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(rw * 4, (int)word);
-    const bool used = rw < p.k || (rw == kRwGate && has_sh);
-    if (f < kRouteReplicas * kRouteWords && used)
-      st64c(line64(p, kLnRoute + f / kRouteWords) + rw, tagged(tag, v));
+    const int w9 = f % 9;
+    const uint32_t val = (uint32_t)__builtin_amdgcn_ds_bpermute(w9 * 4, (int)word);
+    const bool used = w9 < p.k || (w9 == 8 && has_sh);
+    if (f < kRouteReplicas * 9 && used)
+      st64c(route_line(p, f / 9) + (w9 == 8 ? kRwGate : kRwW + w9), tagged(tag, val));
   }
   if (mine) {
     if (p.ids_out) p.ids_out[lane] = my_id;
@@ -383,12 +441,12 @@ __device__ __forceinline__ void task_router(const DecodeParams& p, int t, int la
 // bf16(gate * d_shared).
 __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, int h0, int lane,
                                              const float (&d_last)[kDownRows], uint32_t& rwc, uint32_t tag,
-                                             uint32_t* err) {
+                                             uint32_t* err, RouteLds& L) {
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
   if (!p.ids_in) {
-    const uint64_t need = ((1ull << k) - 1) | (has_sh ? 1ull << kRwGate : 0ull);
-    if (__ballot(rwc == kUnseenWord) & need) route_poll(p, lane, rwc, need, tag, err);
+    const uint32_t slots = (1u << k) - 1u;
+    route_need(p, lane, rwc, (slots << kRwId) | (slots << kRwW) | (has_sh ? 1u << kRwGate : 0u), tag, err, L);
   }
   const int r = lane & (kDownRows - 1);
   // Word j holds this lane's row of slot j (j < k - 1) or, at j = k - 1, of the
@@ -422,10 +480,11 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
 #pragma unroll
   for (int j = 0; j < kFusedMaxK; ++j) {
     if (j >= k) break;
-    const uint32_t rw = (uint32_t)__builtin_amdgcn_readlane((int)rwc, j);
-    const int e = j == k - 1 ? e_last : (int)(rw & 0xFFFFu);
-    if (e < 0 || e >= p.E || rw == kUnseenWord) continue;
-    const float wj = bf16_to_f32((uint16_t)(rw >> 16));
+    const uint32_t rid = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwId + j);
+    const uint32_t rwt = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwW + j);
+    const int e = j == k - 1 ? e_last : (rid == kUnseenWord ? -1 : (int)rid);
+    if (e < 0 || e >= p.E || rwt == kUnseenWord) continue;
+    const float wj = bf16_to_f32((uint16_t)rwt);
     const float d = j == k - 1 ? own : ((r & 1) ? bf16_hi(pr[j]) : bf16_lo(pr[j]));
     acc = rbf16(acc + rbf16(wj * d));
   }
@@ -482,7 +541,7 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
   if (wrap) {
     uint64_t* w = reinterpret_cast<uint64_t*>(p.handoff);
     for (size_t i = lane; i < p.handoff_words; i += 64) st64c(w + i, 0ull);
-    for (int i = lane; i < kRouteReplicas * kLine; i += 64) st32c(line(p, kLnRoute) + i, 0u);
+    for (int i = lane; i < kRouteReplicas * kRouteStride * kLine; i += 64) st32c(line(p, kLnRoute) + i, 0u);
   }
   const uint32_t epoch = wrap ? 0u : tag;
   if (lane < kQueues) st32c(line(p, kLnQueue + lane) + kQueueEpochWord, epoch);
@@ -504,12 +563,22 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   // Every lane loads the epoch (one transaction); kept per lane, the value is
   // first waited for where a task stores or polls.
   const uint32_t tag = ld32c(queue + kQueueEpochWord) + 1u;
-  uint32_t rwc = kUnseenWord;   // this wave's routing cache
-  if (p.ids_in && lane < p.k) {
+  __shared__ RouteLds s_rt;     // the block's view of the routing
+  if (threadIdx.x == 0) {
+    s_rt.valid = 0u;
+    s_rt.poller = 0u;
+  }
+  __syncthreads();
+  uint32_t rwc = kUnseenWord;   // this wave's routing cache (lane layout of RouteWord)
+  if (p.ids_in) {
     // Caller-supplied routing (ids outside [0, E) are skipped; E is the sentinel).
-    const int64_t e = p.ids_in[lane];
-    rwc = ((uint32_t)p.w_in[lane] << 16) | (e >= 0 && e < p.E ? (uint32_t)e : 0xFFFFu);
-    if ((e < 0 || e > p.E) && blockIdx.x == 0 && wid == 0) atomicOr(err, kErrExpertId);
+    if (lane < p.k) {
+      const int64_t e = p.ids_in[lane];
+      rwc = e >= 0 && e < p.E ? (uint32_t)e : 0xFFFFu;
+      if ((e < 0 || e > p.E) && blockIdx.x == 0 && wid == 0) atomicOr(err, kErrExpertId);
+    } else if (lane >= kRwW && lane < kRwW + p.k) {
+      rwc = p.w_in[lane - kRwW];
+    }
   }
   for (uint32_t i = 0;; ++i) {
     // Tickets rank, rank + users, ... of queue q: no atomic between tasks (a wait
@@ -527,7 +596,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     } else if (tk.type == kTS || tk.type == kTG) {
       // Gate/up pairs: the shared expert (S) or routed slot j (G); one call site.
       const bool shared = tk.type == kTS;
-      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err);
+      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
       const int n_rows = shared ? p.Is : p.I;
       const int i0 = tk.idx * kPairs;
       if (e >= 0) {
@@ -540,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     } else {
       // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
-      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err);
+      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
       const int h0 = tk.idx * kDownRows;
       float d[kDownRows] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (e >= 0) {
@@ -559,7 +628,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         if (lane < kDownRows / 2)
           st64c(p.dq64 + ((size_t)(shared ? p.k : tk.slot) * p.H + h0) / 2 + lane, tagged(tag, (uint32_t)pair));
       } else {
-        combine_rows(p, e, h0, lane, d, rwc, tag, err);
+        combine_rows(p, e, h0, lane, d, rwc, tag, err, s_rt);
       }
     }
   }

@@ -140,7 +140,8 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 // Lane L of v takes the wave-uniform value s (v_writelane_b32).
 template <int L>
 __device__ __forceinline__ int set_lane(int v, int s) {
-  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(s), "n"(L));
+  const int su = __builtin_amdgcn_readfirstlane(s);   // the value is wave-uniform; make it scalar
+  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(su), "n"(L));
   return v;
 }
 // Lanes 0..7 take vals[0..7] (wave-uniform values).

@@ -22,22 +22,23 @@ enum ErrorBit { kErrExpertId = 1u, kErrTimeout = 2u };
 // tag}: the tag is the call's epoch, so words left by earlier calls never match
 // and nothing is cleared between calls.
 constexpr int kLine = 64;                 // uint32 per line
-constexpr int kRouteReplicas = 32;        // routing published to this many lines
+constexpr int kRouteReplicas = 32;        // routing published to this many lines ...
+constexpr int kRouteStride = 16;          // ... 16 lines (4 KB) apart, on different memory channels
 constexpr int kQueues = 32;               // task queues: 4 waves x 8 XCD-sized groups of blocks
 enum SyncLine {
   kLnEpoch = 0,                           // word 0: epoch of the next call (tag = epoch + 1)
   kLnQueuesDone = 1,                      // queues fully drained this call
   kLnQueue = 2,                           // [kQueues] word kQueueEpochWord: epoch copy for the queue's waves
   kLnQueueExit = kLnQueue + kQueues,      // [kQueues] waves that left each queue
-  kLnRoute = kLnQueueExit + kQueues,      // [kRouteReplicas] u64 {slot[8], gate}
-  kSyncLines = kLnRoute + kRouteReplicas,
+  kLnRoute = kLnQueueExit + kQueues,      // [kRouteReplicas * kRouteStride] replica r at line r * kRouteStride
+  kSyncLines = kLnRoute + kRouteReplicas * kRouteStride,
 };
 // Each queue line also carries a copy of the epoch, read by that queue's waves
 // (coherent loads of one line serialise, so 2048 waves must not share one word).
 constexpr int kQueueEpochWord = 16;
-// u64 words of a route replica line: slot j = {tag, bf16 weight << 16 | expert id},
-// then the shared-expert gate {tag, bf16 gate}.
-enum RouteWord { kRwSlot = 0, kRwGate = 8, kRouteWords = 9 };
+// u64 words {payload, tag} of a route replica line: the expert ids of slots 0..7,
+// their bf16 weights, the shared-expert bf16 gate.  Ids are published first.
+enum RouteWord { kRwId = 0, kRwW = 8, kRwGate = 16, kRouteWords = 17 };
 
 struct Ws {
   size_t status;   // uint32[kStatusSlots]
