@@ -42,6 +42,18 @@ def prefill_weight_bytes(s):
     return 2 * (E * 3 * H * I + 3 * H * Is)
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes in profiles/<name>."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -70,6 +82,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run plain device copies of known size (scale for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the MoE layer is not sharded across "
@@ -142,13 +156,25 @@ def main():
                    "hidden": H, "experts": shape.num_experts, "intermediate": shape.intermediate,
                    "top_k": shape.top_k, "shared_intermediate": shape.shared_intermediate,
                    "layers_rotated": L, "batch": 1},
-        "roofline": {"kernel": "decode layer (k_decode_a + k_decode_b + k_decode_c on one stream)",
+        "roofline": {"kernel": "k_decode_fused (one persistent launch per token-layer)",
                      "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic("k_decode_fused_decode_h2560_e256_i1024_k8.md"),
                      "algorithmic_bytes_per_launch": nbytes},
         "hbm_gbps": round(gbs, 1),
         "tokens_per_s_48_layers": round(1e6 / (48 * us), 2),
     }
+
+    if args.calibrate_copy:
+        # Plain device copies of a known size: under `rocprofv3 --pmc FETCH_SIZE` /
+        # `WRITE_SIZE` they give the counter-to-byte scale for this GPU.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = src.numel()
+        del src, dst
 
     # ---------------- prefill: T = 4096 through the same layer shape, logits supplied
     if not args.no_prefill:
