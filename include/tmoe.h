@@ -124,6 +124,45 @@ int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float*
                         int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                         void* workspace, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- int4 format (a9)
+ * Packed int4 rows with bf16 group scales, the group-scaled form of the reference's
+ * format (tarfa/engine/channel_q4.py:10-14 dequant_int4, moe_kernel.py:110-114):
+ *   packed [N, K/2] uint8: byte b holds column 2b (low nibble) and 2b+1 (high nibble),
+ *          value = nibble - 8;   scales [N, K/G] bf16;
+ *   dequant  w = bf16((nibble - 8) * scale[n, k / G])
+ * tmoe_quantize_int4 (the reference has no quantiser; its int4 files come from
+ * outside the repository, channel_q4.py:6):
+ *   scale = bf16(max |w| over the group / 7)   (fp32 division, round to nearest even)
+ *   q = clamp(rint(w / scale), -8, 7), q = 0 where scale == 0
+ * w [N, K] bf16.  K a multiple of 8 and of G; G even, at most 2048.
+ * tmoe_dequant_int4_bf16 materialises the bf16 matrix (debug / bit-exact checks);
+ * packed must be 4-byte and out 16-byte aligned.
+ */
+int tmoe_quantize_int4(const void* w, int N, int K, int G, void* packed, void* scales, void* stream);
+int tmoe_dequant_int4_bf16(const void* packed, const void* scales, int N, int K, int G, void* out,
+                           void* stream);
+
+/* ---------------------------------------------------------------- int4 fast mode (a10)
+ * Labelled fast mode of the reference's decode (tarfa/engine/fused_int4.py:206-219 ->
+ * moe_kernel.py:90-104 moe_ffn), with group-128 scales.  Batch 1 only (T == 1),
+ * H and I multiples of 512.  Expert table uint64_t[E][4] (see above), entries
+ * 16-byte aligned.  Per routed expert in router order: fp32 gate/up dot products
+ * (int4 x bf16, fp32 accumulation, group scale applied per group), act =
+ * bf16(silu(g) * u) computed in fp32, fp32 down dot products; then
+ * y = y + w_j * d_j in fp32 (separately rounded products and sums), out = bf16(y).
+ * tmoe_moe_block_int4 adds the router and the shared expert, which stays exact bf16
+ * as in tmoe_moe_block_bf16: out = bf16(bf16(y) + bf16(gate * shared)).  Is == I or 0.
+ * Arguments otherwise as tmoe_experts_forward_bf16 / tmoe_moe_block_bf16.
+ */
+int tmoe_experts_forward_int4(const void* x, int T, const int64_t* ids, const void* weights,
+                              const uint64_t* expert_table_q4, int H, int E, int I, int k, void* out,
+                              void* workspace, size_t ws_bytes, void* stream);
+int tmoe_moe_block_int4(const void* x, int T, const void* router_w, const float* logits_in,
+                        const uint64_t* expert_table_q4, const void* sh_gate, const void* sh_up,
+                        const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k,
+                        int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                        void* workspace, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

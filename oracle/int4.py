@@ -89,3 +89,61 @@ def ffn(x, experts, rw, group=128):
         d = gemv_f32(dq, ds, act, group).astype(np.float64)
         y = (y + (d * np.float64(w)).astype(np.float32)).astype(np.float32).astype(np.float64)
     return rb(y.astype(np.float32))
+
+
+def _act_f64(g, u):
+    """silu(g) * u as ffn evaluates it, before the bf16 rounding (fp32 value, kept in fp64)."""
+    return ((g / (1.0 + np.exp(-g))).astype(np.float32).astype(np.float64) * u).astype(np.float32).astype(np.float64)
+
+
+def ambiguous_roundings(v, rel):
+    """Where v lies within ``rel`` (relative) of a bf16 rounding midpoint: the indices, the
+    bf16 value on the other side of the midpoint (uint16 bits) and the distance to it."""
+    v = np.asarray(v, np.float32)
+    t = v.view(np.uint32) & np.uint32(0xFFFF0000)                   # truncated toward zero
+    lo = t.view(np.float32).astype(np.float64)
+    hi = (t + np.uint32(0x10000)).view(np.float32).astype(np.float64)
+    mid = (lo + hi) / 2
+    dist = np.abs(v.astype(np.float64) - mid)
+    near = (dist <= rel * np.abs(mid)) & np.isfinite(v)
+    tb = (t >> np.uint32(16)).astype(np.uint16)
+    other = np.where(bf16.bits(v) == tb, tb + np.uint16(1), tb).astype(np.uint16)
+    idx = np.nonzero(near)[0]
+    return idx, other[idx], dist[idx]
+
+
+def ffn_candidates(x, experts, rw, group=128, rel=2e-6, max_flips=6):
+    """Every output ``ffn`` can give when each activation lying within ``rel`` of a bf16
+    midpoint may round either way.
+
+    The activation ``bf16(silu(g) * u)`` is the first rounding of the int4 path; g and u
+    are fp32 sums whose last bits depend on the summation order, which the reference
+    leaves to its Triton kernel (moe_kernel.py:54-60).  An activation within a few fp32
+    ulps of a bf16 midpoint can therefore legitimately round either way, and one such
+    flip of a large activation moves every output row by ~1e-3 relative.  Returns a list
+    of bf16 outputs (the first is ``ffn`` itself); at most ``max_flips`` of the closest
+    cases are enumerated.
+    """
+    x = np.asarray(x, np.float32)
+    rw = np.asarray(rw, np.float32).reshape(-1)
+    acts, flips = [], []
+    for j, (gq, gs, dq, ds) in enumerate(experts):
+        gu = gemv_f32(gq, gs, x, group).astype(np.float64)
+        inter = gu.shape[0] // 2
+        a = _act_f64(gu[:inter], gu[inter:]).astype(np.float32)
+        acts.append(rb(a))
+        idx, other, dist = ambiguous_roundings(a, rel)
+        flips += [(float(d), j, int(i), float(bf16.to_f32(o))) for i, o, d in zip(idx, other, dist)]
+    flips = sorted(flips)[:max_flips]
+    outs = []
+    for mask in range(1 << len(flips)):
+        y = np.zeros(x.shape[0], np.float64)
+        for j, (gq, gs, dq, ds) in enumerate(experts):
+            act = acts[j].copy()
+            for b, (_, jj, i, alt) in enumerate(flips):
+                if jj == j and (mask >> b) & 1:
+                    act[i] = alt
+            d = gemv_f32(dq, ds, act, group).astype(np.float64)
+            y = (y + (d * np.float64(rw[j])).astype(np.float32)).astype(np.float32).astype(np.float64)
+        outs.append(rb(y.astype(np.float32)))
+    return outs

@@ -29,6 +29,11 @@ SIGNATURES = {
     "tmoe_experts_forward_bf16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "tmoe_moe_block_bf16": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                  _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tmoe_quantize_int4": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "tmoe_dequant_int4_bf16": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
+    "tmoe_experts_forward_int4": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "tmoe_moe_block_int4": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                 _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _LIB = None

@@ -95,35 +95,51 @@ static void bind_ws(DecodeParams& p, void* ws, size_t ws_bytes, const Ws& L) {
   p.handoff_words = (ws_bytes - L.logits) / 8;
 }
 
-extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
-                                         const uint64_t* expert_table, int H, int E, int I, int k, void* out,
-                                         void* workspace, size_t ws_bytes, void* stream) {
+
+// Int4 mode: T == 1, H and I multiples of 512 (group 128), 16-byte aligned table entries.
+static int experts_forward(const void* x, int T, const int64_t* ids, const void* weights,
+                           const uint64_t* expert_table, int H, int E, int I, int k, void* out, void* workspace,
+                           size_t ws_bytes, hipStream_t s, bool q4) {
   if (int st = check_shape(T, H, E, I, k, 0)) return st;
   if (!x || !ids || !weights || !expert_table || !out || !workspace) return TMOE_ERR_NULL;
   if (misaligned(x) || misaligned(workspace)) return TMOE_ERR_ALIGN;
+  if (q4 && (T != 1 || H % 512 || I % 512)) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, 0);
   if (ws_bytes < L.total) return TMOE_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
   if (T == 1) {
     DecodeParams p{};
     p.x = (const uint16_t*)x;
     p.table = expert_table;
+    p.q4 = q4;
     p.ids_in = ids;
     p.w_in = (const uint16_t*)weights;
     p.H = H; p.E = E; p.I = I; p.k = k; p.Is = 0;
     p.out = (uint16_t*)out;
     bind_ws(p, workspace, ws_bytes, L);
-    return decode(p, false, s);
+    return q4 ? decode_fused_launch(p, false, s) : decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
                         nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s);
 }
 
-extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,
-                                   const uint64_t* expert_table, const void* sh_gate, const void* sh_up,
-                                   const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k, int Is,
-                                   void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
-                                   void* workspace, size_t ws_bytes, void* stream) {
+extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
+                                         const uint64_t* expert_table, int H, int E, int I, int k, void* out,
+                                         void* workspace, size_t ws_bytes, void* stream) {
+  return experts_forward(x, T, ids, weights, expert_table, H, E, I, k, out, workspace, ws_bytes, (hipStream_t)stream,
+                         false);
+}
+
+extern "C" int tmoe_experts_forward_int4(const void* x, int T, const int64_t* ids, const void* weights,
+                                         const uint64_t* expert_table_q4, int H, int E, int I, int k, void* out,
+                                         void* workspace, size_t ws_bytes, void* stream) {
+  return experts_forward(x, T, ids, weights, expert_table_q4, H, E, I, k, out, workspace, ws_bytes,
+                         (hipStream_t)stream, true);
+}
+
+static int moe_block(const void* x, int T, const void* router_w, const float* logits_in, const uint64_t* expert_table,
+                     const void* sh_gate, const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E,
+                     int I, int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                     void* workspace, size_t ws_bytes, hipStream_t s, bool q4) {
   const bool has_sh = sh_gate || sh_up || sh_down || sh_gate_w;
   if (has_sh && (!sh_gate || !sh_up || !sh_down || !sh_gate_w || Is < 8)) return TMOE_ERR_NULL;
   if (!has_sh) Is = 0;
@@ -132,15 +148,16 @@ extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, c
   if (misaligned(x) || misaligned(workspace) || (router_w && misaligned(router_w)) ||
       (has_sh && (misaligned(sh_gate) || misaligned(sh_up) || misaligned(sh_down) || misaligned(sh_gate_w))))
     return TMOE_ERR_ALIGN;
+  if (q4 && (T != 1 || H % 512 || I % 512 || (Is && Is != I))) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, Is);
   if (ws_bytes < L.total) return TMOE_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
   if (T == 1) {
     DecodeParams p{};
     p.x = (const uint16_t*)x;
     p.router_w = logits_in ? nullptr : (const uint16_t*)router_w;
     p.logits_in = logits_in;
     p.table = expert_table;
+    p.q4 = q4;
     p.sh_gate = (const uint16_t*)sh_gate;
     p.sh_up = (const uint16_t*)sh_up;
     p.sh_down = (const uint16_t*)sh_down;
@@ -151,7 +168,7 @@ extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, c
     p.w_out = (uint16_t*)weights_out;
     p.heat = heat;
     bind_ws(p, workspace, ws_bytes, L);
-    return decode(p, true, s);
+    return q4 ? decode_fused_launch(p, true, s) : decode(p, true, s);
   }
   // T > 1: router, shared gate, then the prefill experts path with the shared expert as an extra group.
   float* logits = ws_ptr<float>(workspace, L.logits);
@@ -169,4 +186,22 @@ extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, c
   return prefill_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
                         (const uint16_t*)sh_up, (const uint16_t*)sh_down, has_sh ? gs : nullptr, H, E, I, k, Is,
                         (uint16_t*)out, workspace, s);
+}
+
+extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,
+                                   const uint64_t* expert_table, const void* sh_gate, const void* sh_up,
+                                   const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k, int Is,
+                                   void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  return moe_block(x, T, router_w, logits_in, expert_table, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, out,
+                   ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, false);
+}
+
+extern "C" int tmoe_moe_block_int4(const void* x, int T, const void* router_w, const float* logits_in,
+                                   const uint64_t* expert_table_q4, const void* sh_gate, const void* sh_up,
+                                   const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k, int Is,
+                                   void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  return moe_block(x, T, router_w, logits_in, expert_table_q4, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
+                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, true);
 }

@@ -11,6 +11,11 @@
 //       D(k-1), last in the list, also combines its rows from every slot's tagged
 //       results: acc = bf16(acc + bf16(w_j * d_j)) in router order, then
 //       acc = bf16(acc + bf16(gate * d_shared)), and writes the output.
+// Int4 mode (labelled fast mode) changes the routed tasks only: G takes 4 row
+// pairs of packed int4 rows with fp32 results and act = bf16(silu(g) * u), D takes
+// 16 rows (8 when I > 1024) with fp32 results, and the combine is the fp32 sum
+// y = y + w_j * d_j in router order, cast to bf16 once, plus the bf16 shared expert
+// (tarfa/engine/moe_kernel.py:90-104, fused_int4.py:206-219).
 // ordered R, K, G0 .. G(L), then D(j-L) after each later Gj (L = kDownLag), S
 // after G(kSharedAfter) and SD L slots later, then the remaining D: while the
 // routing resolves only the router rows load, and down rows are drawn only once
@@ -48,6 +53,7 @@
 
 #include "tmoe_decode.h"
 #include "tmoe_gemv.h"
+#include "tmoe_q4.h"
 #include "tmoe_ws.h"
 
 namespace tmoe {
@@ -56,6 +62,9 @@ constexpr int kWaves = 4;              // waves per block
 constexpr int kRouterRows = 4;         // router rows per R task
 constexpr int kPairs = 2;              // gate/up row pairs per G / S task (4 rows of K = H in flight)
 constexpr int kDownRows = 8;           // down rows per D / SD task (8 rows of K = I in flight)
+constexpr int kQ4Pairs = 4;            // int4: gate/up row pairs per G task (8 rows of H/2 bytes)
+// int4: down rows per D task (their scale words, rows * I / 256, fit one per lane)
+constexpr int q4_down_rows(int MI) { return MI <= 2 ? 16 : 8; }
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
@@ -272,6 +281,88 @@ __device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act
 #pragma unroll
     for (int c = 0; c < MI; ++c) acc = dot8p(wr[r][c], af.v[c], acc);
     d[r] = rbf16(wave_sum(acc));
+  }
+}
+
+// Int4 SwiGLU of gate/up row pairs [i0, i0 + 4) of one expert (packed gate_up rows
+// [2I, H/2], scales [2I, H/128]): fp32 gate and up values (no rounding), then
+// act = bf16(silu(g) * u) in fp32 (tarfa/engine/moe_kernel.py:100), published as two
+// tagged bf16 pairs.  Loads in need order: input, scales, then the 8 weight rows.
+template <int MH>
+__device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int i0, int I, int H,
+                                      const uint16_t* x, int lane, uint64_t* act64, uint32_t tag) {
+  constexpr int R = kQ4Pairs;
+  constexpr int G = 4 * MH;    // scale groups per row (H = 512 MH)
+  XPack<MH> xf;
+  load_xpack<MH, true>(xf, x, H, lane);
+  // Scale words of the 4 gate rows and of the 4 up rows: 2G words each, one per lane.
+  const uint32_t* sg = reinterpret_cast<const uint32_t*>(gs + (size_t)i0 * G);
+  const uint32_t* su = reinterpret_cast<const uint32_t*>(gs + (size_t)(I + i0) * G);
+  const uint32_t scg = lane < 2 * G ? sg[lane] : 0u;
+  const uint32_t scu = lane < 2 * G ? su[lane] : 0u;
+  const size_t rowb = (size_t)H / 2;
+  uint32_t w[2 * R][MH];
+#pragma unroll
+  for (int q = 0; q < R; ++q)
+#pragma unroll
+    for (int c = 0; c < MH; ++c) {
+      w[q][c] = ld_stream4(gq + (size_t)(i0 + q) * rowb + c * 256 + lane * 4);
+      w[R + q][c] = ld_stream4(gq + (size_t)(I + i0 + q) * rowb + c * 256 + lane * 4);
+    }
+  Q4Frag<MH> qx;
+  q4_prepare(xf, qx);
+  const uint32_t sel = q4_scale_sel(lane);
+  float v[2 * R];
+#pragma unroll
+  for (int r = 0; r < 2 * R; ++r) {
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < MH; ++c) {
+      const float s = q4_scale(r < R ? scg : scu, ((r % R) * G + 4 * c) / 2 + (lane >> 5), sel);
+      a = fmaf(s, q4_dot8(w[r][c], qx.x[c], qx.off[c]), a);
+    }
+    v[r] = wave_sum(a);
+  }
+  uint32_t pk[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t a0 = f32_to_bf16(silu_f32(v[2 * h]) * v[R + 2 * h]);
+    const uint32_t a1 = f32_to_bf16(silu_f32(v[2 * h + 1]) * v[R + 2 * h + 1]);
+    pk[h] = a0 | (a1 << 16);
+  }
+  if (lane < 2) st64c(act64 + i0 / 2 + lane, tagged(tag, lane ? pk[1] : pk[0]));
+}
+
+// RQ rows of an int4 down projection (packed [H, I/2], scales [H, I/128]):
+// d[r] = fp32 dot(w[h0 + r], act).  Weight rows and activations are requested
+// together, as in down_dots.
+template <int MI, int RQ>
+__device__ __forceinline__ void down_q4(const uint8_t* dq, const uint16_t* ds, const uint64_t* act64, int I, int h0,
+                                        int lane, float (&d)[RQ], uint32_t tag, uint32_t* err) {
+  constexpr int G = 4 * MI;    // scale groups per row (I = 512 MI)
+  static_assert(RQ * G / 2 <= 64, "one scale word per lane");
+  const uint32_t* sp = reinterpret_cast<const uint32_t*>(ds + (size_t)h0 * G);
+  const uint32_t sc = lane < RQ * G / 2 ? sp[lane] : 0u;
+  const size_t rowb = (size_t)I / 2;
+  uint32_t w[RQ][MI];
+#pragma unroll
+  for (int r = 0; r < RQ; ++r)
+#pragma unroll
+    for (int c = 0; c < MI; ++c) w[r][c] = ld_stream4(dq + (size_t)(h0 + r) * rowb + c * 256 + lane * 4);
+  XPack<MI> af;
+  load_acts<MI, true>(af, act64, I, lane, tag, err);
+  Q4Frag<MI> qa;
+  q4_prepare(af, qa);
+  const uint32_t sel = q4_scale_sel(lane);
+#pragma unroll
+  for (int r = 0; r < RQ; ++r) {
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < MI; ++c) {
+      const float s = q4_scale(sc, (r * G + 4 * c) / 2 + (lane >> 5), sel);
+      a = fmaf(s, q4_dot8(w[r][c], qa.x[c], qa.off[c]), a);
+    }
+    d[r] = wave_sum(a);
   }
 }
 
@@ -498,6 +589,67 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
   if (lane < kDownRows) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
+// Int4 mode: the combine of rows h0 .. h0 + RQ - 1 (lane r < RQ owns row h0 + r).
+// Each slot's fp32 row is weighted and summed in fp32 in router order,
+// y = y + w_j * d_j with separately rounded products and sums (the reference's
+// fp32 weighted sum, tarfa/engine/moe_kernel.py:103), cast to bf16 once (:104);
+// then the block adds the bf16 shared expert, bf16(y + bf16(gate * d_shared)).
+template <int RQ>
+__device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, int h0, int lane,
+                                           const float (&d_last)[RQ], uint32_t& rwc, uint32_t tag, uint32_t* err,
+                                           RouteLds& L) {
+  const int k = p.k;
+  const bool has_sh = p.sh_gate != nullptr;
+  if (!p.ids_in) {
+    const uint32_t slots = (1u << k) - 1u;
+    route_need(p, lane, rwc, (slots << kRwId) | (slots << kRwW) | (has_sh ? 1u << kRwGate : 0u), tag, err, L);
+  }
+  const int r = lane & (RQ - 1);
+  uint32_t pr[kFusedMaxK];   // word j: this lane's row of slot j (j < k - 1) or of the shared expert (j = k - 1)
+  Backoff<4> b;
+  for (;;) {
+    uint64_t v[kFusedMaxK];
+#pragma unroll
+    for (int j = 0; j < kFusedMaxK; ++j) {
+      const int slot = j < k - 1 ? j : k;
+      v[j] = ld64c(p.dq64 + (size_t)slot * p.H + h0 + r);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < kFusedMaxK; ++j) {
+      const bool used = j < k - 1 || (j == k - 1 && has_sh);
+      ok &= !used || has_tag(v[j], tag);
+      pr[j] = (uint32_t)v[j];
+    }
+    if (__all(ok)) break;
+    if (!b.step(err)) break;
+  }
+  int rows[RQ];
+#pragma unroll
+  for (int i = 0; i < RQ; ++i) rows[i] = __float_as_int(d_last[i]);
+  const float own = __int_as_float(spread(rows));
+  float y = 0.f;
+#pragma unroll
+  for (int j = 0; j < kFusedMaxK; ++j) {
+    if (j >= k) break;
+    const uint32_t rid = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwId + j);
+    const uint32_t rwt = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwW + j);
+    const int e = j == k - 1 ? e_last : (rid == kUnseenWord ? -1 : (int)rid);
+    if (e < 0 || e >= p.E || rwt == kUnseenWord) continue;
+    const float d = j == k - 1 ? own : __uint_as_float(pr[j]);
+    y = __fadd_rn(y, __fmul_rn(d, bf16_to_f32((uint16_t)rwt)));
+  }
+  float acc = rbf16(y);
+  if (has_sh) {
+    const float g = bf16_to_f32((uint16_t)__builtin_amdgcn_readlane((int)rwc, kRwGate));
+    uint32_t ps = pr[0];
+#pragma unroll
+    for (int j = 1; j < kFusedMaxK; ++j) ps = j == k - 1 ? pr[j] : ps;
+    acc = rbf16(acc + rbf16(g * __uint_as_float(ps)));
+  }
+  if (lane < RQ) p.out[h0 + lane] = f32_to_bf16(acc);
+}
+
 struct TaskRef {
   int type, slot, idx;
 };
@@ -513,25 +665,24 @@ __device__ __forceinline__ TaskRef decode_task(const DecodeParams& p, int t) {
     if (t == 0) return {kTK, 0, 0};
     t -= 1;
   }
-  const int n_sd = p.sh_gate ? p.n_rb : 0;
   for (int j = 0; j < p.k; ++j) {
     if (t < p.n_g) return {kTG, j, t};
     t -= p.n_g;
     if (j >= kDownLag) {
-      if (t < p.n_rb) return {kTD, j - kDownLag, t};
-      t -= p.n_rb;
+      if (t < p.n_d) return {kTD, j - kDownLag, t};
+      t -= p.n_d;
     }
     if (j == p.sh_after) {
       if (t < p.n_s) return {kTS, 0, t};
       t -= p.n_s;
     }
     if (j == p.sd_after) {
-      if (t < n_sd) return {kTSD, p.k, t};
-      t -= n_sd;
+      if (t < p.n_sd) return {kTSD, p.k, t};
+      t -= p.n_sd;
     }
   }
   const int first = p.k > kDownLag ? p.k - kDownLag : 0;
-  return {kTD, first + t / p.n_rb, t % p.n_rb};
+  return {kTD, first + t / p.n_d, t % p.n_d};
 }
 
 // The call is over (every queue drained): advance the epoch.  At the wrap the hand-off area is zeroed first, so tags
@@ -551,9 +702,12 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
   }
 }
 
-template <int MH, int MI, bool EXACT>
+// Q4: routed experts in int4 (table [E][4]); the shared expert stays bf16.
+template <int MH, int MI, bool EXACT, bool Q4>
 __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
-  const int lane = threadIdx.x & 63;
+  static_assert(!Q4 || EXACT, "int4 variants need H and I multiples of 512");
+  constexpr int RQ = q4_down_rows(MI);
+  const int lane0 = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint32_t* err = p.status + kStatusError;
   const int q = (int)(blockIdx.x % 8) * kWaves + wid;
@@ -572,12 +726,12 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   uint32_t rwc = kUnseenWord;   // this wave's routing cache (lane layout of RouteWord)
   if (p.ids_in) {
     // Caller-supplied routing (ids outside [0, E) are skipped; E is the sentinel).
-    if (lane < p.k) {
-      const int64_t e = p.ids_in[lane];
+    if (lane0 < p.k) {
+      const int64_t e = p.ids_in[lane0];
       rwc = e >= 0 && e < p.E ? (uint32_t)e : 0xFFFFu;
       if ((e < 0 || e > p.E) && blockIdx.x == 0 && wid == 0) atomicOr(err, kErrExpertId);
-    } else if (lane >= kRwW && lane < kRwW + p.k) {
-      rwc = p.w_in[lane - kRwW];
+    } else if (lane0 >= kRwW && lane0 < kRwW + p.k) {
+      rwc = p.w_in[lane0 - kRwW];
     }
   }
   for (uint32_t i = 0;; ++i) {
@@ -585,6 +739,10 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     // on a draw would also wait for this wave's stores, which gfx9 counts in vmcnt).
     const int t = q + kQueues * (int)(rank + users * i);
     if (t >= p.n_tasks) break;
+    // The lane index is re-derived per task: otherwise every per-lane address of
+    // every task type is hoisted out of this loop and held in registers throughout.
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
     const TaskRef tk = decode_task(p, t);
     if (tk.type == kTR) {
       task_router<MH, EXACT>(p, tk.idx, lane, tag);
@@ -598,6 +756,13 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       const bool shared = tk.type == kTS;
       const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
       const int n_rows = shared ? p.Is : p.I;
+      if (Q4 && !shared) {
+        if (e >= 0)
+          up_q4<MH>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
+                    reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 1)), tk.idx * kQ4Pairs, p.I, p.H,
+                    p.x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag);
+        continue;
+      }
       const int i0 = tk.idx * kPairs;
       if (e >= 0) {
         const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
@@ -610,6 +775,27 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
       const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
+      if (Q4 && !shared) {
+        const int h0 = tk.idx * RQ;
+        float d[RQ];
+#pragma unroll
+        for (int r = 0; r < RQ; ++r) d[r] = 0.f;
+        if (e >= 0)
+          down_q4<MI, RQ>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
+                          reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 3)),
+                          p.act64 + (size_t)tk.slot * p.I / 2, p.I, h0, lane, d, tag, err);
+        if (tk.slot != p.k - 1) {
+          // One fp32 row per word (a skipped slot publishes zeros the combine ignores).
+          int rows[RQ];
+#pragma unroll
+          for (int r = 0; r < RQ; ++r) rows[r] = __float_as_int(d[r]);
+          const int row = spread(rows);
+          if (lane < RQ) st64c(p.dq64 + (size_t)tk.slot * p.H + h0 + lane, tagged(tag, (uint32_t)row));
+        } else {
+          combine_q4<RQ>(p, e, h0, lane, d, rwc, tag, err, s_rt);
+        }
+        continue;
+      }
       const int h0 = tk.idx * kDownRows;
       float d[kDownRows] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (e >= 0) {
@@ -617,7 +803,14 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         const uint64_t* a = p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2);
         down_dots<MI, EXACT>(w, a, p, shared ? p.Is : p.I, h0, lane, d, tag, err);
       }
-      if (shared || tk.slot != p.k - 1) {
+      if (Q4) {
+        // Int4 mode keeps one row per word: the shared rows as fp32 words of their bf16 values.
+        int rows[kDownRows];
+#pragma unroll
+        for (int r = 0; r < kDownRows; ++r) rows[r] = __float_as_int(d[r]);
+        const int row = spread(rows);
+        if (lane < kDownRows) st64c(p.dq64 + (size_t)p.k * p.H + h0 + lane, tagged(tag, (uint32_t)row));
+      } else if (shared || tk.slot != p.k - 1) {
         // Publish this slot's rows (a skipped slot publishes zeros the combine ignores).
         // Lane q < 4 publishes rows 2q, 2q + 1 (the row values are wave-uniform).
         int pairs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -635,13 +828,13 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   // The last wave to leave queue q re-zeroes its exit count; the last queue to
   // drain ends the call.
   uint32_t fin = 0;
-  if (lane == 0) {
+  if (lane0 == 0) {
     if (add32c(line(p, kLnQueueExit + q), 1u) == users - 1u) {
       st32c(line(p, kLnQueueExit + q), 0u);
       fin = add32c(line(p, kLnQueuesDone), 1u) == (uint32_t)kQueues - 1u;
     }
   }
-  if (__builtin_amdgcn_readfirstlane(fin)) finish_call(p, tag, lane);
+  if (__builtin_amdgcn_readfirstlane(fin)) finish_call(p, tag, lane0);
 }
 
 // ---------------------------------------------------------------- launch
@@ -649,30 +842,45 @@ typedef void (*FusedKernel)(DecodeParams);
 
 // Exact-fit variants (H = 512 MH, I = Is = 512 MI) for the common layer widths;
 // masked variants cover the rest up to H = 4096, I = Is = 2048.
-static FusedKernel pick_fused(int H, int I, int Is) {
+// Int4 mode has exact-fit variants only.
+static FusedKernel pick_fused(int H, int I, int Is, bool q4) {
   if (H % 512 == 0 && I % 512 == 0 && (Is == 0 || Is == I)) {
-    switch ((H / 512) * 10 + I / 512) {
-      case 21: return k_decode_fused<2, 1, true>;
-      case 22: return k_decode_fused<2, 2, true>;
-      case 42: return k_decode_fused<4, 2, true>;
-      case 52: return k_decode_fused<5, 2, true>;
-      case 62: return k_decode_fused<6, 2, true>;
-      case 84: return k_decode_fused<8, 4, true>;
+    const int key = (H / 512) * 10 + I / 512;
+    if (q4) {
+      switch (key) {
+        case 11: return k_decode_fused<1, 1, true, true>;
+        case 21: return k_decode_fused<2, 1, true, true>;
+        case 22: return k_decode_fused<2, 2, true, true>;
+        case 42: return k_decode_fused<4, 2, true, true>;
+        case 52: return k_decode_fused<5, 2, true, true>;
+        case 62: return k_decode_fused<6, 2, true, true>;
+        case 84: return k_decode_fused<8, 4, true, true>;
+      }
+      return nullptr;
+    }
+    switch (key) {
+      case 21: return k_decode_fused<2, 1, true, false>;
+      case 22: return k_decode_fused<2, 2, true, false>;
+      case 42: return k_decode_fused<4, 2, true, false>;
+      case 52: return k_decode_fused<5, 2, true, false>;
+      case 62: return k_decode_fused<6, 2, true, false>;
+      case 84: return k_decode_fused<8, 4, true, false>;
     }
   }
+  if (q4) return nullptr;
   const int inter = I > Is ? I : Is;
   const int ncH = (H + 511) / 512, ncI = (inter + 511) / 512;
   const int mh = ncH <= 2 ? 2 : ncH <= 4 ? 4 : ncH <= 6 ? 6 : ncH <= 8 ? 8 : 0;
   const int mi = ncI <= 2 ? 2 : ncI <= 4 ? 4 : 0;
   switch (mh * 10 + mi) {
-    case 22: return k_decode_fused<2, 2, false>;
-    case 24: return k_decode_fused<2, 4, false>;
-    case 42: return k_decode_fused<4, 2, false>;
-    case 44: return k_decode_fused<4, 4, false>;
-    case 62: return k_decode_fused<6, 2, false>;
-    case 64: return k_decode_fused<6, 4, false>;
-    case 82: return k_decode_fused<8, 2, false>;
-    case 84: return k_decode_fused<8, 4, false>;
+    case 22: return k_decode_fused<2, 2, false, false>;
+    case 24: return k_decode_fused<2, 4, false, false>;
+    case 42: return k_decode_fused<4, 2, false, false>;
+    case 44: return k_decode_fused<4, 4, false, false>;
+    case 62: return k_decode_fused<6, 2, false, false>;
+    case 64: return k_decode_fused<6, 4, false, false>;
+    case 82: return k_decode_fused<8, 2, false, false>;
+    case 84: return k_decode_fused<8, 4, false, false>;
   }
   return nullptr;
 }
@@ -703,19 +911,25 @@ static int resident_blocks(FusedKernel k) {
 
 int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   const bool has_sh = p.sh_gate != nullptr;
-  FusedKernel k = pick_fused(p.H, p.I, p.Is);
+  FusedKernel k = pick_fused(p.H, p.I, p.Is, p.q4 != 0);
   if (!k || p.k > kFusedMaxK || (has_sh && !run_router) || (p.I & 1) || (p.Is & 1) || (p.H % kDownRows))
     return TMOE_ERR_SHAPE;
   const int n_rows = (p.logits_in ? 0 : p.E) + (has_sh ? 1 : 0);
   p.n_r = run_router ? (n_rows > 0 ? (n_rows + kRouterRows - 1) / kRouterRows : 1) : 0;
   p.n_s = has_sh ? (p.Is + kPairs - 1) / kPairs : 0;
-  p.n_g = (p.I + kPairs - 1) / kPairs;
-  p.n_rb = p.H / kDownRows;
+  p.n_sd = has_sh ? p.H / kDownRows : 0;
+  if (p.q4) {
+    p.n_g = p.I / kQ4Pairs;
+    p.n_d = p.H / q4_down_rows(p.I / 512);
+  } else {
+    p.n_g = (p.I + kPairs - 1) / kPairs;
+    p.n_d = p.H / kDownRows;
+  }
   // While the routing resolves only the router rows load: any request issued
   // behind a full memory queue waits microseconds, and every routing step is one.
   p.sh_after = p.k - 1 < kSharedAfter ? p.k - 1 : kSharedAfter;
   p.sd_after = p.k - 1 < p.sh_after + kDownLag ? p.k - 1 : p.sh_after + kDownLag;
-  p.n_tasks = p.n_r + (p.n_r ? 1 : 0) + p.n_s + (has_sh ? p.n_rb : 0) + p.k * (p.n_g + p.n_rb);
+  p.n_tasks = p.n_r + (p.n_r ? 1 : 0) + p.n_s + p.n_sd + p.k * (p.n_g + p.n_d);
   int grid = resident_blocks(k);
   if (grid <= 0) return TMOE_ERR_HIP;
   const int need = (p.n_tasks + kWaves - 1) / kWaves;

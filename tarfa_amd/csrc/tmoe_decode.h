@@ -9,7 +9,8 @@ struct DecodeParams {
   const uint16_t* x;          // [H]
   const uint16_t* router_w;   // [E, H] or null (logits supplied or experts-only mode)
   const float* logits_in;     // [E] or null
-  const uint64_t* table;      // [E][2] gate_up / down base pointers
+  const uint64_t* table;      // [E][2] gate_up / down base pointers; int4: [E][4] (packed, scales) x 2
+  int q4;                     // 1: int4 routed experts (group-128 bf16 scales), fp32 combine
   const uint16_t* sh_gate;    // [Is, H]   (null = no shared expert)
   const uint16_t* sh_up;      // [Is, H]
   const uint16_t* sh_down;    // [H, Is]
@@ -36,10 +37,12 @@ struct DecodeParams {
   uint32_t* sync;             // task-graph lines
   uint64_t* lg64;             // [E + 1] tagged fp32 logits (index E: shared-gate logit)
   uint64_t* act64;            // [k * I / 2] tagged bf16 activation pairs, then [Is / 2] shared
-  uint64_t* dq64;             // [(k + 1) * H / 2] tagged per-slot down pairs (slot k: shared, before its gate)
+  uint64_t* dq64;             // [(k + 1) * H] tagged per-slot down results (slot k: shared, before its gate):
+                              // bf16 row pairs, or one fp32 row per word in int4 mode
   void* handoff;              // workspace past the sync lines: zeroed when the epoch wraps
   size_t handoff_words;       // its size in uint64
-  int n_r, n_s, n_g, n_rb, n_tasks;   // task counts: router, shared up, gate/up per slot, row blocks; total
+  int n_r, n_s, n_g, n_d, n_sd, n_tasks;   // task counts: router, shared up, gate/up per slot, down per slot,
+                                           // shared down; total
   int sh_after, sd_after;     // shared gate/up (S) and shared down (SD) follow these slots' gate/up tasks
 };
 

@@ -157,6 +157,19 @@ __device__ __forceinline__ int spread8(const int (&vals)[8]) {
   v = set_lane<7>(v, vals[7]);
   return v;
 }
+// Lanes 0..N-1 take vals[0..N-1] (wave-uniform values).
+template <int N, int L = 0>
+__device__ __forceinline__ int spread_from(int v, const int (&vals)[N]) {
+  if constexpr (L == N) {
+    return v;
+  } else {
+    return spread_from<N, L + 1>(set_lane<L>(v, vals[L]), vals);
+  }
+}
+template <int N>
+__device__ __forceinline__ int spread(const int (&vals)[N]) {
+  return spread_from<N, 0>(0, vals);
+}
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 __device__ __forceinline__ float sigmoid_f32(float z) { return 1.0f / (1.0f + expf(-z)); }

@@ -54,8 +54,8 @@ struct Ws {
   size_t inv;      // int32[T * k]
   size_t scratch;  // int32[E + 64]      dispatch counters
   size_t ch;       // bf16[T * k * H]    weighted per-assignment expert outputs (T > 1)
-  size_t tagged;   // u64[(E + 1) + (k * I + Is) / 2 + (k + 1) * H / 2]  tagged logits, activation
-                   // pairs, per-slot down pairs (slot k = shared expert)
+  size_t tagged;   // u64[(E + 1) + (k * I + Is) / 2 + (k + 1) * H]  tagged logits, activation
+                   // pairs, per-slot down results (slot k = shared expert)
   size_t total;
 };
 
@@ -80,7 +80,7 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.inv = take(sizeof(int32_t) * t * (size_t)k);
   w.scratch = take(sizeof(int32_t) * (size_t)(E + 64));
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
-  w.tagged = take(8 * ((size_t)(E + 1) + ((size_t)k * I + (size_t)Is) / 2 + (size_t)(k + 1) * H / 2));
+  w.tagged = take(8 * ((size_t)(E + 1) + ((size_t)k * I + (size_t)Is) / 2 + (size_t)(k + 1) * H));
   w.total = o;
   return w;
 }

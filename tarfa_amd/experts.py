@@ -19,7 +19,7 @@ import types
 
 import torch
 
-from .moe import MoEShape, Workspace, expert_table, experts_forward, moe_block
+from .moe import MoEShape, Workspace, expert_table, expert_table_q4, experts_forward, moe_block
 
 
 class ExpertStore:
@@ -33,6 +33,16 @@ class ExpertStore:
     @classmethod
     def from_slabs(cls, shape, gate_up, down):
         return cls(shape, expert_table(gate_up, down), gate_up.device, keepalive=(gate_up, down))
+
+    @classmethod
+    def from_int4(cls, shape, gate_up_q, gate_up_s, down_q, down_s):
+        """Int4 experts (labelled fast mode): packed [E,2I,H/2] / [E,H,I/2] u8, group scales bf16."""
+        ts = (gate_up_q, gate_up_s, down_q, down_s)
+        return cls(shape, expert_table_q4(*ts), gate_up_q.device, keepalive=ts)
+
+    @property
+    def int4(self):
+        return self.table.shape[1] == 4
 
 
 def make_experts_forward(store: ExpertStore):

@@ -82,6 +82,56 @@ def expert_table(gate_up, down):
     return host.to(gate_up.device)
 
 
+def expert_table_q4(gate_up_q, gate_up_s, down_q, down_s):
+    """[E, 4] uint64 device table for int4 experts: packed gate_up [E,2I,H/2] u8, its scales
+    [E,2I,H/128] bf16, packed down [E,H,I/2] u8, its scales [E,H,I/128] bf16."""
+    ts = (gate_up_q, gate_up_s, down_q, down_s)
+    E = gate_up_q.shape[0]
+    for t in ts:
+        if t.shape[0] != E or not t.is_contiguous():
+            raise ValueError("int4 expert tensors must be contiguous with a leading expert dimension")
+    strides = [t.stride(0) * t.element_size() for t in ts]
+    host = torch.tensor([[t.data_ptr() + e * st for t, st in zip(ts, strides)] for e in range(E)],
+                        dtype=torch.int64)
+    if (host % 16).any():
+        raise ValueError("int4 expert slabs must start 16-byte aligned")
+    return host.to(gate_up_q.device)
+
+
+def quantize_int4(w, group=128):
+    """bf16 [..., K] -> (packed [..., K/2] uint8, scales [..., K/group] bf16) on the device."""
+    _need(w, "w", torch.bfloat16)
+    K = w.shape[-1]
+    N = w.numel() // K
+    packed = torch.empty(*w.shape[:-1], K // 2, dtype=torch.uint8, device=w.device)
+    scales = torch.empty(*w.shape[:-1], K // group, dtype=torch.bfloat16, device=w.device)
+    check(lib().tmoe_quantize_int4(_p(w), N, K, group, _p(packed), _p(scales), _stream(w.device)),
+          "tmoe_quantize_int4")
+    return packed, scales
+
+
+def dequant_int4(packed, scales, group=128):
+    """(packed [..., K/2] uint8, scales [..., K/group] bf16) -> bf16 [..., K] (materialised)."""
+    _need(packed, "packed", torch.uint8)
+    _need(scales, "scales", torch.bfloat16, None, packed.device)
+    K = packed.shape[-1] * 2
+    N = packed.numel() * 2 // K
+    if scales.numel() != N * (K // group):
+        raise ValueError("scales do not match packed and group")
+    out = torch.empty(*packed.shape[:-1], K, dtype=torch.bfloat16, device=packed.device)
+    check(lib().tmoe_dequant_int4_bf16(_p(packed), _p(scales), N, K, group, _p(out), _stream(packed.device)),
+          "tmoe_dequant_int4_bf16")
+    return out
+
+
+def _table_kind(table, E, dev):
+    """2 columns: bf16 experts; 4 columns: int4 experts."""
+    _need(table, "expert_table", torch.int64, None, dev)
+    if table.dim() != 2 or table.shape[0] != E or table.shape[1] not in (2, 4):
+        raise ValueError(f"expert_table must be [E, 2] (bf16) or [E, 4] (int4), got {tuple(table.shape)}")
+    return table.shape[1] == 4
+
+
 def router_topk(shape: MoEShape, x=None, router_w=None, logits=None, heat=None):
     """fp32-logit router: returns (ids [T,k] int64, weights [T,k] bf16, logits [T,E] fp32)."""
     H, E, k = shape.hidden, shape.num_experts, shape.top_k
@@ -121,20 +171,24 @@ def dispatch(ids, num_experts, workspace: Workspace):
 
 
 def experts_forward(shape: MoEShape, x, ids, weights, table, workspace: Workspace, out=None):
-    """Routed experts only (the reference's experts.forward); returns out [T,H] bf16."""
+    """Routed experts only (the reference's experts.forward); returns out [T,H] bf16.
+
+    ``table`` [E, 2] selects exact bf16 experts, [E, 4] (expert_table_q4) the int4 fast mode.
+    """
     H, E, I, k = shape.hidden, shape.num_experts, shape.intermediate, shape.top_k
     _need(x, "hidden_states", torch.bfloat16)
     T, dev = x.shape[0], x.device
     _need(x, "hidden_states", torch.bfloat16, (T, H), dev)
     _need(ids, "top_k_index", torch.int64, (T, k), dev)
     _need(weights, "top_k_weights", torch.bfloat16, (T, k), dev)
-    _need(table, "expert_table", torch.int64, (E, 2), dev)
+    q4 = _table_kind(table, E, dev)
     if out is None:
         out = torch.empty_like(x)
     buf = workspace.ensure(T)
-    st = lib().tmoe_experts_forward_bf16(_p(x), T, _p(ids), _p(weights), _p(table), H, E, I, k, _p(out), _p(buf),
-                                         buf.numel(), _stream(dev))
-    check(st, "tmoe_experts_forward_bf16")
+    fn = "tmoe_experts_forward_int4" if q4 else "tmoe_experts_forward_bf16"
+    st = getattr(lib(), fn)(_p(x), T, _p(ids), _p(weights), _p(table), H, E, I, k, _p(out), _p(buf), buf.numel(),
+                            _stream(dev))
+    check(st, fn)
     return out
 
 
@@ -148,7 +202,7 @@ def moe_block(shape: MoEShape, x, table, workspace: Workspace, router_w=None, lo
     _need(x, "hidden_states", torch.bfloat16)
     T, dev = x.shape[0], x.device
     _need(x, "hidden_states", torch.bfloat16, (T, H), dev)
-    _need(table, "expert_table", torch.int64, (E, 2), dev)
+    q4 = _table_kind(table, E, dev)
     if logits is not None:
         _need(logits, "logits", torch.float32, (T, E), dev)
     else:
@@ -171,10 +225,11 @@ def moe_block(shape: MoEShape, x, table, workspace: Workspace, router_w=None, lo
     ids = torch.empty(T, k, dtype=torch.int64, device=dev) if ids is None else ids
     weights = torch.empty(T, k, dtype=torch.bfloat16, device=dev) if weights is None else weights
     buf = workspace.ensure(T)
-    st = lib().tmoe_moe_block_bf16(_p(x), T, _p(router_w) if logits is None else None, _p(logits), _p(table),
-                                   *[_p(t) for t in sh], H, E, I, k, Is if shared is not None else 0, _p(out),
-                                   _p(ids), _p(weights), _p(heat), _p(buf), buf.numel(), _stream(dev))
-    check(st, "tmoe_moe_block_bf16")
+    fn = "tmoe_moe_block_int4" if q4 else "tmoe_moe_block_bf16"
+    st = getattr(lib(), fn)(_p(x), T, _p(router_w) if logits is None else None, _p(logits), _p(table),
+                            *[_p(t) for t in sh], H, E, I, k, Is if shared is not None else 0, _p(out),
+                            _p(ids), _p(weights), _p(heat), _p(buf), buf.numel(), _stream(dev))
+    check(st, fn)
     return out, ids, weights
 
 

@@ -40,3 +40,10 @@ def expert_dicts(gate_up, down, ids):
         for j, e in enumerate(uniq):
             gu[e], dn[e] = g[j], d[j]
     return gu, dn
+
+
+def assert_close_any_bf16(got, refs, what=""):
+    """assert_close_bf16 against the closest of several admissible oracle outputs (the
+    oracle enumerates activations that lie on a bf16 rounding midpoint within fp32 error)."""
+    best = min(range(len(refs)), key=lambda i: rel_l2(got, refs[i]))
+    return assert_close_bf16(got, refs[best], f"{what} (candidate {best} of {len(refs)})")

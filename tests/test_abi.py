@@ -55,3 +55,17 @@ def test_entry_points_reject_bad_arguments_without_touching_the_device():
     assert lib.tmoe_router_topk(None, None, None, 1, 2560, 256, 17, None, None, None, None, None) == -2
     assert lib.tmoe_dispatch(None, 4, 8, 256, None, None, None, None, 0, None) == -1
     assert lib.tmoe_fill_bf16(None, 16, 1, 1.0, 0, None) == -1
+    # int4 entry points: NULLs and unsupported shapes (T > 1, H or I not a multiple of 512, bad group)
+    assert lib.tmoe_experts_forward_int4(None, 1, None, None, None, 2560, 256, 1024, 8, None, None, 0, None) == -1
+    assert lib.tmoe_moe_block_int4(None, 1, None, None, None, None, None, None, None, 2560, 256, 1024, 8, 0,
+                                   None, None, None, None, None, 0, None) == -1
+    p = 256   # any non-NULL, 16-byte aligned value: rejected before it is dereferenced
+    assert lib.tmoe_experts_forward_int4(p, 2, p, p, p, 2560, 256, 1024, 8, p, p, 1 << 30, None) == -2
+    assert lib.tmoe_experts_forward_int4(p, 1, p, p, p, 2304, 256, 1024, 8, p, p, 1 << 30, None) == -2
+    assert lib.tmoe_moe_block_int4(p, 1, p, None, p, p, p, p, p, 2560, 256, 1024, 8, 512,
+                                   p, None, None, None, p, 1 << 30, None) == -2        # Is != I
+    assert lib.tmoe_quantize_int4(None, 4, 256, 128, None, None, None) == -1
+    assert lib.tmoe_quantize_int4(p, 4, 256, 96, p, p, None) == -2                    # K % G
+    assert lib.tmoe_quantize_int4(p, 4, 256, 3, p, p, None) == -2                     # odd G
+    assert lib.tmoe_dequant_int4_bf16(p, p, 4, 260, 130, p, None) == -2               # K % 8
+    assert lib.tmoe_dequant_int4_bf16(p + 2, p, 4, 256, 128, p, None) == -3           # packed alignment

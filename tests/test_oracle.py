@@ -348,3 +348,33 @@ def test_int4_ffn_group_form_equals_rowscale_form_when_scales_repeat():
     a = _ffn_rowscale(x, gup, gus, dp, ds, rw)
     b = int4.ffn(x, [(gup[e], np.repeat(gus[e], 2, -1), dp[e], ds[e]) for e in range(E)], rw, group=128)
     assert rel_l2(a, b) < 1e-6
+
+
+def test_int4_ambiguous_roundings_known_answers():
+    v = np.array([1.12109375 + 1e-7, 1.12107, 1.5, -1.12109375 - 2e-7, 3.0, 1.0], np.float32)
+    idx, other, dist = int4.ambiguous_roundings(v, 2e-6)
+    assert list(idx) == [0, 3]
+    # 1.12109375 is the midpoint of bf16 1.1171875 (0x3F8F) and 1.125 (0x3F90)
+    assert bf16.bits(v[0]) == 0x3F90 and other[0] == 0x3F8F
+    assert bf16.bits(v[3]) == 0xBF90 and other[1] == 0xBF8F
+    assert np.all(dist < 3e-7)
+    idx, _, _ = int4.ambiguous_roundings(v, 0.0)
+    assert idx.size == 0
+
+
+def test_int4_ffn_candidates_first_is_ffn_and_count():
+    g = np.random.default_rng(3)
+    H, I, E = 256, 128, 3
+    ex = []
+    for e in range(E):
+        gq, gs = int4.quantize(g.standard_normal((2 * I, H)).astype(np.float32) * 0.02, 128)
+        dq, ds = int4.quantize(g.standard_normal((H, I)).astype(np.float32) * 0.02, 128)
+        ex.append((gq, gs, dq, ds))
+    x = bf16.rnd(g.standard_normal(H).astype(np.float32))
+    rw = bf16.rnd(np.array([0.5, 0.3, 0.2], np.float32))
+    outs = int4.ffn_candidates(x, ex, rw)
+    assert np.array_equal(outs[0], int4.ffn(x, ex, rw))
+    # every activation "ambiguous": 2^max_flips candidates
+    outs = int4.ffn_candidates(x, ex, rw, rel=1.0, max_flips=2)
+    assert len(outs) == 4
+    assert np.array_equal(outs[0], int4.ffn(x, ex, rw))
