@@ -8,11 +8,12 @@ layer; steps rotate over ``--layers`` distinct seeded layers and fresh tokens so
 the per-step working set (~143 MB) is never served from the 256 MB Infinity
 Cache.  Inputs and weights are resident in HBM before timing starts.
 
-Also reported: the T=4096 exact-BF16 prefill chunk through the same layer shape
-(router logits supplied ~N(0,1)), and the reference's op sequence run on the
-host CPU (torch bf16) on a bounded sample as ``cpu_baseline``.
+Also reported: the labelled int4 fast mode at the same shape (``int4``), the
+T=4096 exact-BF16 prefill chunk through the same layer shape (router logits
+supplied ~N(0,1)), and the reference's op sequence run on the host CPU (torch
+bf16) on a bounded sample as ``cpu_baseline``.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-int4]
 """
 import argparse
 import json
@@ -30,6 +31,14 @@ def decode_bytes(s):
     """Algorithmic bytes of one decode token-layer: 8 routed experts, shared expert, router, shared gate."""
     H, E, I, k, Is = s.hidden, s.num_experts, s.intermediate, s.top_k, s.shared_intermediate
     return 2 * (k * 3 * H * I + 3 * H * Is + E * H + (H if Is else 0))
+
+
+def decode_bytes_int4(s, group=128):
+    """Algorithmic bytes of one int4 fast-mode token-layer: 8 routed experts as packed int4 plus
+    bf16 group scales, the bf16 shared expert, router and shared gate."""
+    H, E, I, k, Is = s.hidden, s.num_experts, s.intermediate, s.top_k, s.shared_intermediate
+    per_expert = 3 * H * I // 2 + 2 * (3 * H * I // group)
+    return k * per_expert + 2 * (3 * H * Is + E * H + (H if Is else 0))
 
 
 def prefill_flops(s, T):
@@ -82,6 +91,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-int4", action="store_true")
+    ap.add_argument("--int4-steps", type=int, default=2000)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain device copies of known size (scale for HBM byte counters)")
     args = ap.parse_args()
@@ -175,6 +186,48 @@ def main():
         torch.cuda.synchronize()
         result["copy_calibration_bytes"] = src.numel()
         del src, dst
+
+    # ---------------- int4 fast mode: the same layers with their routed experts quantised (group 128)
+    if not args.no_int4:
+        t0 = time.perf_counter()
+        q4 = []
+        for ly in layers:
+            gq, gsc = tm.quantize_int4(ly.gate_up)
+            dq, dsc = tm.quantize_int4(ly.down)
+            q4.append((gq, gsc, dq, dsc))
+        q4_tables = [tm.expert_table_q4(*q) for q in q4]
+        torch.cuda.synchronize()
+        log(f"int4 setup {time.perf_counter() - t0:.1f}s")
+        fn4 = lib().tmoe_moe_block_int4
+        K4 = args.int4_steps
+
+        def args_q4(l, r):
+            a = list(args_for(l, r))
+            a[4] = q4_tables[l].data_ptr()
+            return tuple(a)
+
+        plan4 = [args_q4(s % L, s // L) for s in range(W + K4)]
+        for a in plan4[:W]:
+            fn4(*a)
+        torch.cuda.synchronize()
+        e0.record()
+        for a in plan4[W:]:
+            if fn4(*a):
+                raise RuntimeError("tmoe_moe_block_int4 failed")
+        e1.record()
+        torch.cuda.synchronize()
+        ws.status()
+        us4 = e0.elapsed_time(e1) * 1e3 / K4
+        nb4 = decode_bytes_int4(shape)
+        gbs4 = nb4 / (us4 * 1e-6) / 1e9
+        result["int4"] = {"workload": "labelled int4 fast mode at the same layer shape, batch 1: routed experts "
+                                      "int4 [-8,7] packed 2 per byte along K, bf16 scales per group of 128 "
+                                      "(max|w|/7), shared expert exact bf16",
+                          "us_per_token_layer": round(us4, 3), "hbm_gbps": round(gbs4, 1),
+                          "frac": round(gbs4 / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nb4,
+                          "steps": K4, "tokens_per_s_48_layers": round(1e6 / (48 * us4), 2)}
+        log(f"int4 decode: {us4:.2f} us/token-layer, {gbs4:.0f} GB/s")
+        del q4, q4_tables, plan4
 
     # ---------------- prefill: T = 4096 through the same layer shape, logits supplied
     if not args.no_prefill:

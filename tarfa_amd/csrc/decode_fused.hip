@@ -63,7 +63,7 @@ constexpr int kRouterRows = 4;         // router rows per R task
 constexpr int kPairs = 2;              // gate/up row pairs per G / S task (4 rows of K = H in flight)
 constexpr int kDownRows = 8;           // down rows per D / SD task (8 rows of K = I in flight)
 constexpr int kQ4Pairs = 4;            // int4: gate/up row pairs per G task (8 rows of H/2 bytes)
-// int4: down rows per D task (their scale words, rows * I / 256, fit one per lane)
+// int4: down rows per D task (their scale words, rows * I / 256, fit two per lane)
 constexpr int q4_down_rows(int MI) { return MI <= 2 ? 16 : 8; }
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
@@ -284,22 +284,27 @@ __device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act
   }
 }
 
-// Int4 SwiGLU of gate/up row pairs [i0, i0 + 4) of one expert (packed gate_up rows
+// Int4 SwiGLU of gate/up row pairs [i0, i0 + R) of one expert (packed gate_up rows
 // [2I, H/2], scales [2I, H/128]): fp32 gate and up values (no rounding), then
-// act = bf16(silu(g) * u) in fp32 (tarfa/engine/moe_kernel.py:100), published as two
-// tagged bf16 pairs.  Loads in need order: input, scales, then the 8 weight rows.
-template <int MH>
+// act = bf16(silu(g) * u) in fp32 (tarfa/engine/moe_kernel.py:100), published as R/2
+// tagged bf16 pairs.  Loads in need order: input, scales, then the 2R weight rows.
+template <int MH, int R>
 __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int i0, int I, int H,
                                       const uint16_t* x, int lane, uint64_t* act64, uint32_t tag) {
-  constexpr int R = kQ4Pairs;
-  constexpr int G = 4 * MH;    // scale groups per row (H = 512 MH)
+  constexpr int G = 4 * MH;            // scale groups per row (H = 512 MH)
+  constexpr int NW = R * G / 2;        // scale words of R rows
+  static_assert(R % 2 == 0 && NW <= 128, "scale words of a block fit two per lane");
   XPack<MH> xf;
   load_xpack<MH, true>(xf, x, H, lane);
-  // Scale words of the 4 gate rows and of the 4 up rows: 2G words each, one per lane.
+  // Scale words of the R gate rows and of the R up rows: word i of a block in lane i % 64, register i / 64.
   const uint32_t* sg = reinterpret_cast<const uint32_t*>(gs + (size_t)i0 * G);
   const uint32_t* su = reinterpret_cast<const uint32_t*>(gs + (size_t)(I + i0) * G);
-  const uint32_t scg = lane < 2 * G ? sg[lane] : 0u;
-  const uint32_t scu = lane < 2 * G ? su[lane] : 0u;
+  uint32_t sc[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    sc[0][h] = (h * 64 < NW && lane + h * 64 < NW) ? sg[lane + h * 64] : 0u;
+    sc[1][h] = (h * 64 < NW && lane + h * 64 < NW) ? su[lane + h * 64] : 0u;
+  }
   const size_t rowb = (size_t)H / 2;
   uint32_t w[2 * R][MH];
 #pragma unroll
@@ -318,19 +323,21 @@ __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int
     float a = 0.f;
 #pragma unroll
     for (int c = 0; c < MH; ++c) {
-      const float s = q4_scale(r < R ? scg : scu, ((r % R) * G + 4 * c) / 2 + (lane >> 5), sel);
-      a = fmaf(s, q4_dot8(w[r][c], qx.x[c], qx.off[c]), a);
+      // Words base, base + 1 (base even: G is a multiple of 4) share one register.
+      const int base = ((r % R) * G + 4 * c) / 2;
+      a = fmaf(q4_scale(sc[r / R][base / 64], (base % 64) + (lane >> 5), sel), q4_dot8(w[r][c], qx.x[c], qx.off[c]), a);
     }
     v[r] = wave_sum(a);
   }
-  uint32_t pk[2];
+  int pk[R / 2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < R / 2; ++h) {
     const uint32_t a0 = f32_to_bf16(silu_f32(v[2 * h]) * v[R + 2 * h]);
     const uint32_t a1 = f32_to_bf16(silu_f32(v[2 * h + 1]) * v[R + 2 * h + 1]);
-    pk[h] = a0 | (a1 << 16);
+    pk[h] = (int)(a0 | (a1 << 16));
   }
-  if (lane < 2) st64c(act64 + i0 / 2 + lane, tagged(tag, lane ? pk[1] : pk[0]));
+  const uint32_t word = (uint32_t)spread(pk);
+  if (lane < R / 2) st64c(act64 + i0 / 2 + lane, tagged(tag, word));
 }
 
 // RQ rows of an int4 down projection (packed [H, I/2], scales [H, I/128]):
@@ -339,10 +346,13 @@ __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int
 template <int MI, int RQ>
 __device__ __forceinline__ void down_q4(const uint8_t* dq, const uint16_t* ds, const uint64_t* act64, int I, int h0,
                                         int lane, float (&d)[RQ], uint32_t tag, uint32_t* err) {
-  constexpr int G = 4 * MI;    // scale groups per row (I = 512 MI)
-  static_assert(RQ * G / 2 <= 64, "one scale word per lane");
+  constexpr int G = 4 * MI;            // scale groups per row (I = 512 MI)
+  constexpr int NW = RQ * G / 2;       // scale words of the RQ rows
+  static_assert(NW <= 128, "scale words fit two per lane");
   const uint32_t* sp = reinterpret_cast<const uint32_t*>(ds + (size_t)h0 * G);
-  const uint32_t sc = lane < RQ * G / 2 ? sp[lane] : 0u;
+  uint32_t sc[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) sc[h] = (h * 64 < NW && lane + h * 64 < NW) ? sp[lane + h * 64] : 0u;
   const size_t rowb = (size_t)I / 2;
   uint32_t w[RQ][MI];
 #pragma unroll
@@ -359,8 +369,8 @@ __device__ __forceinline__ void down_q4(const uint8_t* dq, const uint16_t* ds, c
     float a = 0.f;
 #pragma unroll
     for (int c = 0; c < MI; ++c) {
-      const float s = q4_scale(sc, (r * G + 4 * c) / 2 + (lane >> 5), sel);
-      a = fmaf(s, q4_dot8(w[r][c], qa.x[c], qa.off[c]), a);
+      const int base = (r * G + 4 * c) / 2;   // even: words base, base + 1 share one register
+      a = fmaf(q4_scale(sc[base / 64], (base % 64) + (lane >> 5), sel), q4_dot8(w[r][c], qa.x[c], qa.off[c]), a);
     }
     d[r] = wave_sum(a);
   }
@@ -650,6 +660,31 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
   if (lane < RQ) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
+// Int4 mode, a D task of routed slot j: RQ rows published as one fp32 word each (a
+// skipped slot publishes zeros the combine ignores), or combined for the last slot.
+template <int MI, int RQ>
+__device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, int idx, int lane, uint32_t& rwc,
+                                             uint32_t tag, uint32_t* err, RouteLds& L) {
+  const int e = wave_slot_expert(p, slot, lane, rwc, tag, err, L);
+  const int h0 = idx * RQ;
+  float d[RQ];
+#pragma unroll
+  for (int r = 0; r < RQ; ++r) d[r] = 0.f;
+  if (e >= 0)
+    down_q4<MI, RQ>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
+                    reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 3)), p.act64 + (size_t)slot * p.I / 2,
+                    p.I, h0, lane, d, tag, err);
+  if (slot != p.k - 1) {
+    int rows[RQ];
+#pragma unroll
+    for (int r = 0; r < RQ; ++r) rows[r] = __float_as_int(d[r]);
+    const int row = spread(rows);
+    if (lane < RQ) st64c(p.dq64 + (size_t)slot * p.H + h0 + lane, tagged(tag, (uint32_t)row));
+  } else {
+    combine_q4<RQ>(p, e, h0, lane, d, rwc, tag, err, L);
+  }
+}
+
 struct TaskRef {
   int type, slot, idx;
 };
@@ -758,44 +793,22 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       const int n_rows = shared ? p.Is : p.I;
       if (Q4 && !shared) {
         if (e >= 0)
-          up_q4<MH>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
+          up_q4<MH, kQ4Pairs>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 1)), tk.idx * kQ4Pairs, p.I, p.H,
                     p.x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag);
-        continue;
-      }
-      const int i0 = tk.idx * kPairs;
-      if (e >= 0) {
+      } else if (e >= 0) {
         const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
         const uint16_t* g = shared ? p.sh_gate : gu;
         const uint16_t* u = shared ? p.sh_up : gu + (size_t)p.I * p.H;
-        up_pairs<MH, EXACT>(g, u, i0, n_rows, p.H, p.x, lane,
+        up_pairs<MH, EXACT>(g, u, tk.idx * kPairs, n_rows, p.H, p.x, lane,
                             p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag);
       }
+    } else if (Q4 && tk.type == kTD) {
+      task_down_q4<MI, RQ>(p, tk.slot, tk.idx, lane, rwc, tag, err, s_rt);
     } else {
       // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
       const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
-      if (Q4 && !shared) {
-        const int h0 = tk.idx * RQ;
-        float d[RQ];
-#pragma unroll
-        for (int r = 0; r < RQ; ++r) d[r] = 0.f;
-        if (e >= 0)
-          down_q4<MI, RQ>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
-                          reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 3)),
-                          p.act64 + (size_t)tk.slot * p.I / 2, p.I, h0, lane, d, tag, err);
-        if (tk.slot != p.k - 1) {
-          // One fp32 row per word (a skipped slot publishes zeros the combine ignores).
-          int rows[RQ];
-#pragma unroll
-          for (int r = 0; r < RQ; ++r) rows[r] = __float_as_int(d[r]);
-          const int row = spread(rows);
-          if (lane < RQ) st64c(p.dq64 + (size_t)tk.slot * p.H + h0 + lane, tagged(tag, (uint32_t)row));
-        } else {
-          combine_q4<RQ>(p, e, h0, lane, d, rwc, tag, err, s_rt);
-        }
-        continue;
-      }
       const int h0 = tk.idx * kDownRows;
       float d[kDownRows] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (e >= 0) {
