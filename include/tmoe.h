@@ -163,6 +163,24 @@ int tmoe_moe_block_int4(const void* x, int T, const void* router_w, const float*
                         int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                         void* workspace, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- route telemetry (a13)
+ * The reference's per-layer route-reuse counters (tarfa/engine/fused_int4.py:71-95
+ * _record_route / routing_telemetry), kept on the device so decode never synchronises
+ * the host for telemetry.  `state` is a zero-filled device buffer of
+ * tmoe_route_telemetry_bytes(L, k, E) bytes (8-byte aligned); one tmoe_route_record call
+ * per token records ids [L, k] int64 (each layer's routing, e.g. the ids_out of its
+ * tmoe_moe_block_* call).  Per layer: ids outside [0, E) are dropped (the sentinel E
+ * included); a step without a valid id records nothing; otherwise steps += 1,
+ * uses += number of valid ids, reuse_w += |set(ids) & union of the last w recorded
+ * sets| for w = 1, 2, 4, 8, 16, distinct += newly seen experts.  The state begins with
+ * uint64 counters[L][8] = {steps, uses, reuse_1, reuse_2, reuse_4, reuse_8, reuse_16,
+ * distinct}.  Heat counters per (layer, expert) are the `heat` argument of the block
+ * entry points.
+ */
+size_t tmoe_route_telemetry_bytes(int L, int k, int E);
+int tmoe_route_record(const int64_t* ids, int L, int k, int E, void* state, size_t state_bytes,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

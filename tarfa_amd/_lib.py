@@ -34,6 +34,8 @@ SIGNATURES = {
     "tmoe_experts_forward_int4": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "tmoe_moe_block_int4": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                  _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tmoe_route_telemetry_bytes": (_sz, [_i, _i, _i]),
+    "tmoe_route_record": (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
 }
 
 _LIB = None
@@ -49,7 +51,9 @@ def _hip_runtimes_mapped():
 
 
 def lib():
-    """The loaded library (loaded on first use)."""
+    """The loaded library (loaded on first use).  Every exported entry point gets its
+    argument types from SIGNATURES: an unbound name raises instead of being called with
+    ctypes' default int arguments."""
     global _LIB
     if _LIB is not None:
         return _LIB
@@ -62,11 +66,24 @@ def lib():
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype, fn.argtypes = res, args
+    handle = _Bound(handle)
     v = handle.tmoe_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libtmoe ABI {v}, expected {ABI_VERSION}: rebuild with `python -m tarfa_amd.build`")
     _LIB = handle
     return handle
+
+
+class _Bound:
+    """The library handle, restricted to the entry points with declared signatures."""
+
+    def __init__(self, handle):
+        self._handle = handle
+        for name in SIGNATURES:
+            setattr(self, name, getattr(handle, name))
+
+    def __getattr__(self, name):
+        raise AttributeError(f"libtmoe entry point {name} has no signature in tarfa_amd._lib.SIGNATURES")
 
 
 def check(status, what):

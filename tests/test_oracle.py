@@ -378,3 +378,60 @@ def test_int4_ffn_candidates_first_is_ffn_and_count():
     outs = int4.ffn_candidates(x, ex, rw, rel=1.0, max_flips=2)
     assert len(outs) == 4
     assert np.array_equal(outs[0], int4.ffn(x, ex, rw))
+
+
+# ------------------------------------------------------------------ route telemetry (a13)
+def test_route_telemetry_known_answers():
+    """Hand-worked sequence through the restatement of fused_int4.py:71-84."""
+    from oracle.telemetry import RouteTelemetry
+    t = RouteTelemetry(2)
+    E = 10
+    t.record(0, [1, 2, 3], E)            # nothing seen before
+    t.record(0, [3, 4, 10], E)           # 10 = sentinel dropped; 3 reused from 1 step back
+    t.record(0, [10, 10, 10], E)         # all sentinel: not recorded
+    t.record(0, [1, 4, 5], E)            # 4 one back, 1 two back
+    t.record(1, [7, 7, 8], E)            # list of 3 uses, set of 2
+    st = t.per_layer[0]
+    assert st["decode_steps"] == 3 and st["expert_uses"] == 3 + 2 + 3
+    assert st["reuse_1"] == 1 + 1 and st["reuse_2"] == 1 + 2 and st["reuse_16"] == 3
+    assert t.per_layer[1]["expert_uses"] == 3 and t.per_layer[1]["reuse_1"] == 0
+    tot = t.totals()
+    assert tot["unique_layer_experts"] == 5 + 2
+    # 17 steps later expert 1 falls out of every window
+    for s in range(16):
+        t.record(0, [9], E)
+    before = t.per_layer[0]["reuse_16"]
+    t.record(0, [1], E)
+    assert t.per_layer[0]["reuse_16"] == before
+
+
+def test_expert_bytes_match_the_workload_definition():
+    from tarfa_amd.moe import MoEShape
+    from tarfa_amd.residency import expert_bytes
+    s = MoEShape(2560, 256, 1024, 8, 1024)
+    assert expert_bytes(s) == 15_728_640             # 3 x 2560 x 1024 x 2 B
+    assert expert_bytes(s, int4=True) == 4_055_040   # 3,932,160 packed + 122,880 scale bytes
+
+
+def test_zipf_logits_follow_the_rank_weights():
+    """Gumbel-top-k of log w + Gumbel samples without replacement with P proportional to w:
+    the empirical top-1 frequency of each expert matches w / sum(w) (chi-square-level check)."""
+    import torch
+    from tarfa_amd.moe import MoEShape
+    from tarfa_amd.residency import zipf_logits
+    s = MoEShape(64, 32, 8, 4)
+    T = 20000
+    lg, ranks = zipf_logits(s, 2, T, seed=7, device="cpu")
+    assert lg.shape == (T, 2, 32) and lg.dtype == torch.float32
+    top1 = lg.argmax(-1)                                     # [T, L]
+    w = (ranks.double() + 1.0) ** -1.1                       # [L, E]
+    p = (w / w.sum(-1, keepdim=True)).numpy()
+    for l in range(2):
+        freq = np.bincount(top1[:, l].numpy(), minlength=32) / T
+        assert np.all(np.abs(freq - p[l]) < 5 * np.sqrt(p[l] * (1 - p[l]) / T) + 1e-3)
+    # popularity by rank is monotone in the k-selection counts too (top-4 of 32)
+    sel = torch.zeros(2, 32)
+    for l in range(2):
+        sel[l].scatter_add_(0, lg[:, l].topk(4, -1).indices.reshape(-1), torch.ones(T * 4))
+        by_rank = sel[l][torch.argsort(ranks[l])]
+        assert by_rank[0] > by_rank[4] > by_rank[16] > by_rank[31]
