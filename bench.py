@@ -6,14 +6,16 @@ layer (H=2560, E=256 routed experts with I=1024, top-8, one shared expert with
 Is=1024), router included, µs per token-layer.  A step is one token through one
 layer; steps rotate over ``--layers`` distinct seeded layers and fresh tokens so
 the per-step working set (~143 MB) is never served from the 256 MB Infinity
-Cache.  Inputs and weights are resident in HBM before timing starts.
+Cache.  Inputs and weights are resident in HBM before timing starts: the 48 layers
+(194 GB of bf16 experts) live in one residency ledger.
 
 Also reported: the labelled int4 fast mode at the same shape (``int4``), the
+48-layer stack decoding consecutive tokens with Zipf-popular routing (``stack``), the
 T=4096 exact-BF16 prefill chunk through the same layer shape (router logits
 supplied ~N(0,1)), and the reference's op sequence run on the host CPU (torch
 bf16) on a bounded sample as ``cpu_baseline``.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-int4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-int4] [--no-stack]
 """
 import argparse
 import json
@@ -86,7 +88,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=48,
+                    help="resident seeded layers (48 = the whole stack, 194 GB of bf16 experts)")
+    ap.add_argument("--stack-tokens", type=int, default=64)
+    ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--cpu-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
@@ -106,6 +111,8 @@ def main():
     from tarfa_amd import moe as tm
     from tarfa_amd._lib import lib
     from tarfa_amd.moe import MoEShape, Workspace
+    from tarfa_amd.residency import LayerWeights, ResidencyLedger, zipf_logits
+    from tarfa_amd.stack import MoEStack
 
     dev = torch.device("cuda:0")
     shape = MoEShape(2560, 256, 1024, 8, 1024)
@@ -113,10 +120,18 @@ def main():
     H = shape.hidden
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
-    # ---------------- setup: L seeded full-size layers and per-layer token streams, all in HBM
+    # ---------------- setup: the L seeded full-size layers resident in HBM (residency ledger),
+    # per-layer router / shared-expert weights and token streams
     t0 = time.perf_counter()
-    layers = [seeded.make_layer(shape, seed=1, layer=l, device=dev) for l in range(L)]
-    tables = [tm.expert_table(ly.gate_up, ly.down) for ly in layers]
+    ledger = ResidencyLedger(shape, L, dev)
+    ledger.fill_seeded(1)
+
+    class _Layer:
+        def __init__(self, l):
+            self.router_w, self.shared = seeded.make_block_weights(shape, 1, l, dev)
+
+    layers = [_Layer(l) for l in range(L)]
+    tables = [ledger.tables[l] for l in range(L)]
     per_layer = (K + W + L - 1) // L + 1
     xs = [seeded.make_tokens(shape, 1, per_layer, layer=l, device=dev) for l in range(L)]
     ws = Workspace(shape, dev)
@@ -124,7 +139,7 @@ def main():
     ids = torch.empty(1, shape.top_k, dtype=torch.int64, device=dev)
     wts = torch.empty(1, shape.top_k, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
-    log(f"setup {time.perf_counter() - t0:.1f}s: {L} layers x {prefill_weight_bytes(shape) / 1e9:.2f} GB")
+    log(f"setup {time.perf_counter() - t0:.1f}s: {L} resident layers x {prefill_weight_bytes(shape) / 1e9:.2f} GB")
 
     # Lean launch path: prebuilt ctypes arguments, one C call per step.
     fn = lib().tmoe_moe_block_bf16
@@ -190,13 +205,8 @@ def main():
     # ---------------- int4 fast mode: the same layers with their routed experts quantised (group 128)
     if not args.no_int4:
         t0 = time.perf_counter()
-        q4 = []
-        for ly in layers:
-            gq, gsc = tm.quantize_int4(ly.gate_up)
-            dq, dsc = tm.quantize_int4(ly.down)
-            q4.append((gq, gsc, dq, dsc))
-        q4_tables = [tm.expert_table_q4(*q) for q in q4]
-        torch.cuda.synchronize()
+        q4 = ResidencyLedger.quantized_from(ledger)
+        q4_tables = [q4.tables[l] for l in range(L)]
         log(f"int4 setup {time.perf_counter() - t0:.1f}s")
         fn4 = lib().tmoe_moe_block_int4
         K4 = args.int4_steps
@@ -270,13 +280,48 @@ def main():
         log(f"prefill: {pus:.1f} us/layer, {tflops:.1f} TFLOP/s, weights {wgbs:.0f} GB/s")
         del pws
 
+    # ---------------- the whole stack: 48 resident layers, batch-1 decode of consecutive tokens,
+    # per-layer router logits with Zipf(1.1) expert popularity (heat ledger + route telemetry on)
+    if not args.no_stack:
+        NT, NW = args.stack_tokens, 4
+        blocks = [LayerWeights(ly.router_w, ly.shared) for ly in layers]
+        stack = MoEStack(ledger, blocks)
+        ledger.heat.zero_()
+        slg, _ = zipf_logits(shape, L, NT + NW, seed=11, device=dev)
+        sx = seeded.make_tokens(shape, 3, NT + NW, device=dev)
+        for t in range(NW):
+            stack.decode(sx[t:t + 1], slg[t])
+        torch.cuda.synchronize()
+        e0.record()
+        for t in range(NW, NW + NT):
+            stack.decode(sx[t:t + 1], slg[t])
+        e1.record()
+        torch.cuda.synchronize()
+        stack.status()
+        ms_tok = e0.elapsed_time(e1) / NT
+        # logits are supplied: per layer the routed experts, the shared expert and the shared gate row are read
+        tok_bytes = L * (decode_bytes(shape) - 2 * shape.num_experts * H)
+        heat = ledger.heat.cpu()
+        top8 = heat.sort(-1, descending=True).values[:, :8].sum(-1).double() / heat.sum(-1).double()
+        result["stack"] = {"workload": f"{L}-layer MoE-only stack at the full-size layer shape, {194.1 * L / 48:.1f} GB of "
+                                       "experts resident in HBM, batch-1 decode of consecutive tokens; per-layer "
+                                       "router logits log(Zipf s=1.1 weight of a permuted rank) + Gumbel",
+                           "layers": L, "tokens": NT, "ms_per_token": round(ms_tok, 4),
+                           "tokens_per_s": round(1e3 / ms_tok, 2), "us_per_layer": round(ms_tok * 1e3 / L, 3),
+                           "hbm_gbps": round(tok_bytes / (ms_tok * 1e-3) / 1e9, 1),
+                           "algorithmic_bytes_per_token": tok_bytes,
+                           "heat_top8_share_mean": round(float(top8.mean()), 4),
+                           "routing_telemetry": stack.telemetry.routing_telemetry()}
+        log(f"stack: {ms_tok:.3f} ms/token over {L} layers")
+        del stack
+
     # ---------------- CPU baseline: the reference's op chain in torch bf16 on the host
     if not args.no_cpu:
         from oracle import cpu_reference as cref
         nt = cpu_threads()
         torch.set_num_threads(nt)
         ly = layers[0]
-        gu, dn = ly.gate_up.cpu(), ly.down.cpu()
+        gu, dn = ledger.hbm[0][0].cpu(), ledger.hbm[0][1].cpu()
         wg = ly.router_w.cpu()
         shw = tuple(t.cpu() for t in ly.shared)
         xc = xs[0][:args.cpu_tokens].cpu()

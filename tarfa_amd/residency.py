@@ -150,6 +150,19 @@ class ResidencyLedger:
                 self._store(l, e0, parts)
         torch.cuda.synchronize(dev)
 
+    @classmethod
+    def quantized_from(cls, src: "ResidencyLedger"):
+        """A fully resident int4 ledger holding the group-quantised experts of a resident bf16 ledger."""
+        if src.int4 or src.tiered:
+            raise ValueError("quantise from a fully resident bf16 ledger")
+        q = cls(src.shape, src.L, src.device, int4=True)
+        g = src.shape.group_size
+        for l in range(src.L):
+            for dst, part in zip(q.hbm[l], (*quantize_int4(src.hbm[l][0], g), *quantize_int4(src.hbm[l][1], g))):
+                dst.copy_(part)
+        torch.cuda.synchronize(src.device)
+        return q
+
     def load_layer(self, layer, parts):
         """Copy a layer's experts from full tensors ([E, ...] per part, any device)."""
         self._store(layer, 0, [p.to(self.device) if not self.tiered else p for p in parts])

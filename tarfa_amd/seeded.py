@@ -74,6 +74,15 @@ def make_layer(shape, seed, layer=0, device="cuda", gate_up=None, down=None):
     gate_up = torch.empty(E, 2 * I, H, **bf) if gate_up is None else gate_up
     down = torch.empty(E, H, I, **bf) if down is None else down
     fill_expert_slabs(gate_up, down, seed, layer)
+    router_w, shared = make_block_weights(shape, seed, layer, device)
+    return SeededLayer(gate_up, down, router_w, shared)
+
+
+def make_block_weights(shape, seed, layer=0, device="cuda"):
+    """The router and shared-expert weights of one layer (same streams as make_layer)."""
+    from .moe import fill_bf16
+    H, E, Is = shape.hidden, shape.num_experts, shape.shared_intermediate
+    bf = dict(dtype=torch.bfloat16, device=device)
     router_w = fill_bf16(torch.empty(E, H, **bf), key(seed, KIND_ROUTER, layer), W_STD)
     shared = None
     if Is:
@@ -81,7 +90,7 @@ def make_layer(shape, seed, layer=0, device="cuda", gate_up=None, down=None):
                   fill_bf16(torch.empty(Is, H, **bf), key(seed, KIND_SH_UP, layer), W_STD),
                   fill_bf16(torch.empty(H, Is, **bf), key(seed, KIND_SH_DOWN, layer), W_STD),
                   fill_bf16(torch.empty(H, **bf), key(seed, KIND_SH_GATEW, layer), W_STD))
-    return SeededLayer(gate_up, down, router_w, shared)
+    return router_w, shared
 
 
 def make_tokens(shape, seed, tokens, layer=0, device="cuda"):
