@@ -13,15 +13,18 @@ rng     counter-based seeded generator (splitmix64 finaliser, Irwin-Hall normal
 moe     router (fp32 logits, softmax, top-k, renorm), dispatch permutation,
         exact-BF16 expert SwiGLU for decode and prefill, shared expert, combine.
 int4    builder-defined group-128 quantiser, dequantiser and the fused
-        dequant-GEMV FFN semantics of the int4 fast mode.
+        dequant-GEMV FFN semantics of the int4 fast mode, with the
+        enumeration of activations that sit on a bf16 rounding midpoint.
+telemetry  route-reuse counters of the reference's decode telemetry.
+cpu_reference  the reference's op chain in torch CPU bf16 (CPU baseline, pin).
 
 Every function cites the reference file:line it restates.  Paths
 ``tarfa/...`` are in the reference repository; ``transformers/...`` is the
 third-party package (5.15.0) that the reference calls for its router and shared
 expert.
 
-Pinning status (each function is checked in ``tests/test_oracle_*.py`` against
-something other than its own formula):
+Pinning status (each function is checked in ``tests/test_oracle.py`` and
+``tests/test_golden.py`` against something other than its own formula):
 
 * bf16 rounding       pinned: torch ``Tensor.to(bfloat16)`` on 2^24 patterns + edge cases.
 * rng                 pinned: moments, determinism, device bit-equality (GPU test).
@@ -34,4 +37,6 @@ something other than its own formula):
 * int4 quantiser      pinned by invariants only (the reference ships no quantiser).
 * int4 ffn            pinned: reference ``_ref_ffn`` closed form (``moe_kernel.py:117-125``)
                       reimplemented in torch fp64 with per-row scales (group = K).
+* int4 ffn_candidates pinned: known answers at bf16 midpoints; first candidate == ffn.
+* telemetry           pinned: a hand-worked sequence of steps (fused_int4.py:71-84).
 """
