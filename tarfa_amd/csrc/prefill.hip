@@ -18,9 +18,11 @@ namespace tmoe {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kBM = 256;        // rows per M-chunk: a whole group in one block up to 256 rows
+constexpr int kBM = 160;        // rows per M-chunk: a whole group in one block up to 160 rows
+constexpr int kAS = kBM / 32;   // A rows staged per thread (rows tid/8 + 32 i)
 constexpr int kBK = 64;         // K per LDS stage
 constexpr int kLdsStride = 72;  // bf16 per LDS row (64 + 8 pad: spreads rows over banks)
+constexpr int kRing = 4;        // K stages of A and of the weights requested ahead of the multiply
 
 __device__ __forceinline__ int load_id(const int32_t* ids32, const int64_t* ids64, size_t i) {
   return ids32 ? ids32[i] : (int)ids64[i];
@@ -155,7 +157,9 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_ca
 
 // Block = 4 waves; tile = (up to 256 rows of one group) x (two 16-row weight sets per
 // wave).  A is staged through LDS (double-buffered, one barrier per 64-wide K stage);
-// weights are read once, straight into MFMA B-fragment registers one stage ahead.
+// weights are read once, straight into MFMA B-fragment registers, kRing stages ahead.
+// RING = K stages requested ahead (the launcher picks kRing when K / 64 > kRing, else 1).
+template <int RING>
 __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][kBM * kLdsStride];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -205,10 +209,12 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
   const uint16_t* b0 = w0 + bl;
   const uint16_t* b1 = w1 + bl;
 
-  // A rows this thread stages: rows tid/8 + 32 i, 16-byte column chunk tid % 8.
-  const uint16_t* arow[8];
+  // A rows this thread stages: rows tid/8 + 32 i, 16-byte column chunk tid % 8.  Rows past
+  // the group repeat its last row, so every load is unconditional (results of those rows
+  // are never written).
+  const uint16_t* arow[kAS];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kAS; ++i) {
     const int r = (tid >> 3) + 32 * i;
     const int rr = r0 + min(r, m - 1);
     size_t row;
@@ -219,61 +225,87 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
   const int lds_st = (tid >> 3) * kLdsStride + (tid & 7) * 8;   // + 32 * i * kLdsStride
   const int lds_ld = (lane & 15) * kLdsStride + 8 * (lane >> 4); // + sub*16*kLdsStride + ks*32
 
-  f32x4 acc[16][2];
+  constexpr int kSubs = kBM / 16;
+  f32x4 acc[kSubs][2];
 #pragma unroll
-  for (int s = 0; s < 16; ++s) acc[s][0] = acc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < kSubs; ++s) acc[s][0] = acc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 areg[8], breg[2][2];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if ((tid >> 3) + 32 * i < m) areg[i] = ld16(arow[i]);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    breg[ks][0] = ld_stream(b0 + 32 * ks);
-    breg[ks][1] = ld_stream(b1 + 32 * ks);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if ((tid >> 3) + 32 * i < m) *reinterpret_cast<u32x4*>(&lds[0][lds_st + 32 * i * kLdsStride]) = areg[i];
-  __syncthreads();
-
+  // Software pipeline over K stages of 64: A rows for stages s + 1 .. s + kRing and weight
+  // fragments for stages s .. s + kRing - 1 are in flight while stage s multiplies.  A
+  // stage waits in registers until its LDS buffer frees (double-buffered); weights go
+  // straight from registers into the MFMA.  Ring slots are static (the loops are
+  // unrolled by kRing), and the loads of the main rounds are unconditional, so the
+  // compiler's in-order count of outstanding loads stays exact and each wait is for one
+  // stage only; the last stages run in a guarded tail.
+  u32x4 areg[RING][kAS], breg[RING][2][2];
   const int nk = K / kBK;
-  for (int st = 0; st < nk; ++st) {
-    const int cur = st & 1;
-    const bool more = st + 1 < nk;
-    u32x4 an[8], bn[2][2];
-    if (more) {
-      const int k0 = (st + 1) * kBK;
+  auto load_a = [&](int slot, int st) {
+    const int k0 = st * kBK;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if ((tid >> 3) + 32 * i < m) an[i] = ld16(arow[i] + k0);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        bn[ks][0] = ld_stream(b0 + k0 + 32 * ks);
-        bn[ks][1] = ld_stream(b1 + k0 + 32 * ks);
-      }
-    }
+    for (int i = 0; i < kAS; ++i) areg[slot][i] = ld16(arow[i] + k0);
+  };
+  auto load_b = [&](int slot, int st) {
+    const int k0 = st * kBK;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8_t bg = as_bf16x8(breg[ks][0]), bu = as_bf16x8(breg[ks][1]);
+      breg[slot][ks][0] = ld_stream(b0 + k0 + 32 * ks);
+      breg[slot][ks][1] = ld_stream(b1 + k0 + 32 * ks);
+    }
+  };
+  auto store_a = [&](int buf, int slot) {
 #pragma unroll
-      for (int sub = 0; sub < 16; ++sub) {
+    for (int i = 0; i < kAS; ++i)
+      *reinterpret_cast<u32x4*>(&lds[buf][lds_st + 32 * i * kLdsStride]) = areg[slot][i];
+  };
+  auto multiply = [&](int buf, int slot) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8_t bg = as_bf16x8(breg[slot][ks][0]), bu = as_bf16x8(breg[slot][ks][1]);
+#pragma unroll
+      for (int sub = 0; sub < kSubs; ++sub) {
         if (sub * 16 < m) {
-          const u32x4 av = *reinterpret_cast<const u32x4*>(&lds[cur][lds_ld + sub * 16 * kLdsStride + ks * 32]);
+          const u32x4 av = *reinterpret_cast<const u32x4*>(&lds[buf][lds_ld + sub * 16 * kLdsStride + ks * 32]);
           const bf16x8_t a = as_bf16x8(av);
           acc[sub][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bg, acc[sub][0], 0, 0, 0);
           acc[sub][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bu, acc[sub][1], 0, 0, 0);
         }
       }
     }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if ((tid >> 3) + 32 * i < m) *reinterpret_cast<u32x4*>(&lds[cur ^ 1][lds_st + 32 * i * kLdsStride]) = an[i];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) { breg[ks][0] = bn[ks][0]; breg[ks][1] = bn[ks][1]; }
+  };
+  // One K stage st (ring slot u = st % RING): stage st + 1's A to the other LDS buffer
+  // (last read before the previous barrier) and its register slot refilled with stage
+  // st + 1 + RING; multiply stage st; refill its weight slot with stage st + RING.
+  auto stage = [&](int u, int st, bool more_a, bool more_b) {
+    if (st + 1 < nk) {
+      store_a((st + 1) & 1, (u + 1) % RING);
+      if (more_a) load_a((u + 1) % RING, st + 1 + RING);
     }
+    multiply(st & 1, u);
+    if (more_b) load_b(u, st + RING);
     __syncthreads();
+  };
+  // Prologue (the launcher guarantees nk >= RING + 1): stages 0 .. RING - 1 requested,
+  // stage 0 staged in LDS, its register slot refilled with stage RING.
+#pragma unroll
+  for (int st = 0; st < RING; ++st) {
+    load_a(st, st);
+    load_b(st, st);
+  }
+  store_a(0, 0);
+  load_a(0, RING);
+  __syncthreads();
+  // Main rounds: every stage st < n_main has both refills in range.
+  const int n_main = (nk - RING - 1) / RING * RING;
+  for (int st0 = 0; st0 < n_main; st0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; ++u) stage(u, st0 + u, true, true);
+  }
+  for (int st0 = n_main; st0 < nk; st0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; ++u) {
+      const int st = st0 + u;
+      if (st < nk) stage(u, st, st + 1 + RING < nk, st + RING < nk);
+    }
   }
 
   // Epilogue.  C fragment: lane l holds rows 4*(l/16) + i, column l % 16.
@@ -282,7 +314,7 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
   if (p.up) {
     uint16_t* o = p.out + (size_t)(shared ? p.shared_row0 + r0 : grow0 + r0) * p.N + col;
 #pragma unroll
-    for (int sub = 0; sub < 16; ++sub)
+    for (int sub = 0; sub < kSubs; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = sub * 16 + rl + i;
@@ -292,7 +324,7 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
   } else if (shared) {
     uint16_t* o = p.out_sh + (size_t)r0 * p.N + col;
 #pragma unroll
-    for (int sub = 0; sub < 16; ++sub)
+    for (int sub = 0; sub < kSubs; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = sub * 16 + rl + i;
@@ -304,7 +336,7 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
     uint16_t* o = p.out + (size_t)(grow0 + r0) * p.N + col;
     const int32_t* pr = p.perm + grow0 + r0;
 #pragma unroll
-    for (int sub = 0; sub < 16; ++sub)
+    for (int sub = 0; sub < kSubs; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = sub * 16 + rl + i;
@@ -391,7 +423,8 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
                    void* ws, hipStream_t s) {
   const bool has_sh = sh_gate != nullptr;
-  if (H % 128 || I % 64 || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
+  // K stages of 64: each GEMM needs at least two (a ring of one stage ahead).
+  if (H % 128 || I % 64 || I < 2 * kBK || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, Is);
   int32_t* offsets = ws_ptr<int32_t>(ws, L.offsets);
   int32_t* perm = ws_ptr<int32_t>(ws, L.perm);
@@ -412,13 +445,14 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   up.T = T; up.E = E; up.k = k; up.n_groups = n_groups; up.n_ntiles = I / 64; up.up = 1; up.N = I; up.I = I;
   up.table = table; up.shw0 = sh_gate; up.shw1 = sh_up; up.shared_row0 = T * k; up.out = act;
   long gu = (mbound * up.n_ntiles + 7) / 8 * 8;
-  hipLaunchKernelGGL(k_grouped_gemm, dim3((unsigned)gu), dim3(256), 0, s, up);
+  auto gemm = [](int K) { return K / kBK > kRing ? k_grouped_gemm<kRing> : k_grouped_gemm<1>; };
+  hipLaunchKernelGGL(gemm(H), dim3((unsigned)gu), dim3(256), 0, s, up);
 
   GemmParams dn = up;
   dn.a = act; dn.K = I; dn.gather = 0; dn.n_ntiles = H / 128; dn.up = 0; dn.N = H;
   dn.shw0 = sh_down; dn.shw1 = nullptr; dn.out = ch; dn.out_sh = sh; dn.wf = wf; dn.wb = wb; dn.gs = gs;
   long gd = (mbound * dn.n_ntiles + 7) / 8 * 8;
-  hipLaunchKernelGGL(k_grouped_gemm, dim3((unsigned)gd), dim3(256), 0, s, dn);
+  hipLaunchKernelGGL(gemm(I), dim3((unsigned)gd), dim3(256), 0, s, dn);
 
   const int nc = (H + 511) / 512;
   const dim3 gc((T + 3) / 4), bc(256);
