@@ -158,7 +158,7 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_ca
 // Block = 4 waves; tile = (up to 256 rows of one group) x (two 16-row weight sets per
 // wave).  A is staged through LDS (double-buffered, one barrier per 64-wide K stage);
 // weights are read once, straight into MFMA B-fragment registers, kRing stages ahead.
-// RING = K stages requested ahead (the launcher picks kRing when K / 64 > kRing, else 1).
+// RING = K stages requested ahead of the multiply.
 template <int RING>
 __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][kBM * kLdsStride];
@@ -230,13 +230,11 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
 #pragma unroll
   for (int s = 0; s < kSubs; ++s) acc[s][0] = acc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Software pipeline over K stages of 64: A rows for stages s + 1 .. s + kRing and weight
-  // fragments for stages s .. s + kRing - 1 are in flight while stage s multiplies.  A
+  // Software pipeline over K stages of 64: A rows for stages s + 1 .. s + RING and weight
+  // fragments for stages s .. s + RING - 1 are in flight while stage s multiplies.  An A
   // stage waits in registers until its LDS buffer frees (double-buffered); weights go
-  // straight from registers into the MFMA.  Ring slots are static (the loops are
-  // unrolled by kRing), and the loads of the main rounds are unconditional, so the
-  // compiler's in-order count of outstanding loads stays exact and each wait is for one
-  // stage only; the last stages run in a guarded tail.
+  // straight from registers into the MFMA.  Ring slots are static (the loop is unrolled
+  // by RING).
   u32x4 areg[RING][kAS], breg[RING][2][2];
   const int nk = K / kBK;
   auto load_a = [&](int slot, int st) {
@@ -257,54 +255,54 @@ __global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
     for (int i = 0; i < kAS; ++i)
       *reinterpret_cast<u32x4*>(&lds[buf][lds_st + 32 * i * kLdsStride]) = areg[slot][i];
   };
+  // All kSubs 16-row sub-tiles every stage, straight-line: the A fragments of a 32-wide k
+  // step are read from LDS before their MFMAs issue (one LDS round trip per k step), and
+  // the accumulators keep one register assignment.  Sub-tiles past the group's rows
+  // multiply repeated rows whose results are never written; at ~128 rows per group that
+  // is a quarter more MFMA work, well under the time the weight stream takes.
   auto multiply = [&](int buf, int slot) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const bf16x8_t bg = as_bf16x8(breg[slot][ks][0]), bu = as_bf16x8(breg[slot][ks][1]);
+      u32x4 av[kSubs];
+#pragma unroll
+      for (int sub = 0; sub < kSubs; ++sub)
+        av[sub] = *reinterpret_cast<const u32x4*>(&lds[buf][lds_ld + sub * 16 * kLdsStride + ks * 32]);
 #pragma unroll
       for (int sub = 0; sub < kSubs; ++sub) {
-        if (sub * 16 < m) {
-          const u32x4 av = *reinterpret_cast<const u32x4*>(&lds[buf][lds_ld + sub * 16 * kLdsStride + ks * 32]);
-          const bf16x8_t a = as_bf16x8(av);
-          acc[sub][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bg, acc[sub][0], 0, 0, 0);
-          acc[sub][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bu, acc[sub][1], 0, 0, 0);
-        }
+        const bf16x8_t a = as_bf16x8(av[sub]);
+        acc[sub][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bg, acc[sub][0], 0, 0, 0);
+        acc[sub][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bu, acc[sub][1], 0, 0, 0);
       }
     }
   };
-  // One K stage st (ring slot u = st % RING): stage st + 1's A to the other LDS buffer
-  // (last read before the previous barrier) and its register slot refilled with stage
-  // st + 1 + RING; multiply stage st; refill its weight slot with stage st + RING.
-  auto stage = [&](int u, int st, bool more_a, bool more_b) {
-    if (st + 1 < nk) {
-      store_a((st + 1) & 1, (u + 1) % RING);
-      if (more_a) load_a((u + 1) % RING, st + 1 + RING);
-    }
-    multiply(st & 1, u);
-    if (more_b) load_b(u, st + RING);
-    __syncthreads();
-  };
-  // Prologue (the launcher guarantees nk >= RING + 1): stages 0 .. RING - 1 requested,
-  // stage 0 staged in LDS, its register slot refilled with stage RING.
+  // Every refill is unconditional: a stage index past the end is clamped to the last
+  // stage (a repeat of addresses just read, served by the L2), so the compiler's
+  // in-order count of outstanding loads stays exact and each wait covers one stage;
+  // only the multiply (LDS reads and MFMA, no global loads) sits behind a branch.
+  const int last = nk - 1;
+  // Prologue: stages 0 .. RING - 1 requested, stage 0 staged in LDS, its register slot
+  // refilled with stage RING.
 #pragma unroll
   for (int st = 0; st < RING; ++st) {
-    load_a(st, st);
-    load_b(st, st);
+    load_a(st, min(st, last));
+    load_b(st, min(st, last));
   }
   store_a(0, 0);
-  load_a(0, RING);
+  load_a(0, min(RING, last));
   __syncthreads();
-  // Main rounds: every stage st < n_main has both refills in range.
-  const int n_main = (nk - RING - 1) / RING * RING;
-  for (int st0 = 0; st0 < n_main; st0 += RING) {
-#pragma unroll
-    for (int u = 0; u < RING; ++u) stage(u, st0 + u, true, true);
-  }
-  for (int st0 = n_main; st0 < nk; st0 += RING) {
+  // Stage st (ring slot u = st % RING): stage st + 1's A to the other LDS buffer (last
+  // read before the previous barrier), its register slot refilled with stage
+  // st + 1 + RING; multiply stage st; refill its weight slot with stage st + RING.
+  for (int st0 = 0; st0 < nk; st0 += RING) {
 #pragma unroll
     for (int u = 0; u < RING; ++u) {
       const int st = st0 + u;
-      if (st < nk) stage(u, st, st + 1 + RING < nk, st + RING < nk);
+      store_a((st + 1) & 1, (u + 1) % RING);
+      load_a((u + 1) % RING, min(st + 1 + RING, last));
+      if (st < nk) multiply(st & 1, u);
+      load_b(u, min(st + RING, last));
+      __syncthreads();
     }
   }
 
@@ -423,8 +421,7 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
                    void* ws, hipStream_t s) {
   const bool has_sh = sh_gate != nullptr;
-  // K stages of 64: each GEMM needs at least two (a ring of one stage ahead).
-  if (H % 128 || I % 64 || I < 2 * kBK || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
+  if (H % 128 || I % 64 || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, Is);
   int32_t* offsets = ws_ptr<int32_t>(ws, L.offsets);
   int32_t* perm = ws_ptr<int32_t>(ws, L.perm);
@@ -445,14 +442,13 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   up.T = T; up.E = E; up.k = k; up.n_groups = n_groups; up.n_ntiles = I / 64; up.up = 1; up.N = I; up.I = I;
   up.table = table; up.shw0 = sh_gate; up.shw1 = sh_up; up.shared_row0 = T * k; up.out = act;
   long gu = (mbound * up.n_ntiles + 7) / 8 * 8;
-  auto gemm = [](int K) { return K / kBK > kRing ? k_grouped_gemm<kRing> : k_grouped_gemm<1>; };
-  hipLaunchKernelGGL(gemm(H), dim3((unsigned)gu), dim3(256), 0, s, up);
+  hipLaunchKernelGGL(k_grouped_gemm<kRing>, dim3((unsigned)gu), dim3(256), 0, s, up);
 
   GemmParams dn = up;
   dn.a = act; dn.K = I; dn.gather = 0; dn.n_ntiles = H / 128; dn.up = 0; dn.N = H;
   dn.shw0 = sh_down; dn.shw1 = nullptr; dn.out = ch; dn.out_sh = sh; dn.wf = wf; dn.wb = wb; dn.gs = gs;
   long gd = (mbound * dn.n_ntiles + 7) / 8 * 8;
-  hipLaunchKernelGGL(gemm(I), dim3((unsigned)gd), dim3(256), 0, s, dn);
+  hipLaunchKernelGGL(k_grouped_gemm<kRing>, dim3((unsigned)gd), dim3(256), 0, s, dn);
 
   const int nc = (H + 511) / 512;
   const dim3 gc((T + 3) / 4), bc(256);
