@@ -22,7 +22,8 @@ constexpr int kBM = 160;        // rows per M-chunk: a whole group in one block 
 constexpr int kAS = kBM / 32;   // A rows staged per thread (rows tid/8 + 32 i)
 constexpr int kBK = 64;         // K per LDS stage
 constexpr int kLdsStride = 72;  // bf16 per LDS row (64 + 8 pad: spreads rows over banks)
-constexpr int kRing = 4;        // K stages of A and of the weights requested ahead of the multiply
+constexpr int kRing = 3;        // K stages of A and of the weights requested ahead of the multiply
+                                // (3 keeps a wave within 256 registers: two blocks per CU)
 
 __device__ __forceinline__ int load_id(const int32_t* ids32, const int64_t* ids64, size_t i) {
   return ids32 ? ids32[i] : (int)ids64[i];
@@ -160,7 +161,7 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_ca
 // weights are read once, straight into MFMA B-fragment registers, kRing stages ahead.
 // RING = K stages requested ahead of the multiply.
 template <int RING>
-__global__ __launch_bounds__(256, 1) void k_grouped_gemm(GemmParams p) {
+__global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][kBM * kLdsStride];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
 
