@@ -239,3 +239,35 @@ def test_prefill_group_larger_than_one_tile(gpu):
     gu, dn = expert_dicts(layer.gate_up, layer.down, ids.cpu().numpy())
     ref = moe.experts_prefill(f32(x), ids.cpu().numpy(), f32(w), gu, dn, 8)
     assert_close_bf16(f32(out), ref, "skewed prefill")
+
+
+@pytest.mark.parametrize("E,k", [(32, 8), (256, 8), (8, 8), (16, 4), (512, 8)])
+def test_decode_router_exact_ties(gpu, E, k):
+    """The fused decode's in-kernel top-k on supplied logits with many exact ties (and +-0):
+    ids bit-exact against the oracle's order (logit descending, ties to the lower index)."""
+    shape = MoEShape(1024, E, 512, k, 0)
+    layer = seeded.make_layer(shape, 12, device=gpu)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    ws = Workspace(shape, gpu)
+    x = seeded.make_tokens(shape, 12, 1, device=gpu)
+    rng = np.random.default_rng(E + k)
+    vals = np.array([0.0, -0.0, 1.5, -2.25, 3.0, 1.5, 0.75], np.float32)
+    for trial in range(8):
+        lg = rng.choice(vals, size=E).astype(np.float32)
+        if trial == 0:
+            lg[:] = 0.0
+            lg[::2] = -0.0                          # every logit tied (+0 and -0 compare equal)
+        if trial == 1:
+            lg = np.arange(E, dtype=np.float32) % 3  # tied blocks across every lane position
+        out, ids, w = tm.moe_block(shape, x, table, ws, logits=torch.from_numpy(lg[None].copy()).to(gpu))
+        ids_ref, w_ref, _ = moe.router_topk(lg[None], k)
+        assert np.array_equal(ids.cpu().numpy(), ids_ref), f"E={E} k={k} trial {trial}"
+        assert np.all(np.abs(f32(w) - w_ref) <= np.abs(w_ref) * 2.0 ** -7)
+    # fewer finite logits than slots: the rest take the sentinel E with weight 0
+    lg = np.full(E, -np.inf, np.float32)
+    lg[[5, 2, 7]] = [1.0, 1.0, 0.5]
+    out, ids, w = tm.moe_block(shape, x, table, ws, logits=torch.from_numpy(lg[None].copy()).to(gpu))
+    want = [2, 5, 7] + [E] * (k - 3)
+    assert ids.cpu().numpy()[0].tolist() == want
+    assert np.all(f32(w)[0, 3:] == 0) and abs(float(f32(w)[0, :3].sum()) - 1.0) < 1e-2
+    ws.status()
