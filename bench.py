@@ -235,6 +235,7 @@ def main():
                                       "(max|w|/7), shared expert exact bf16",
                           "us_per_token_layer": round(us4, 3), "hbm_gbps": round(gbs4, 1),
                           "frac": round(gbs4 / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nb4,
+                          "traffic": profiled_traffic("k_decode_fused_int4_decode_h2560_e256_i1024_k8.md"),
                           "steps": K4, "tokens_per_s_48_layers": round(1e6 / (48 * us4), 2)}
         log(f"int4 decode: {us4:.2f} us/token-layer, {gbs4:.0f} GB/s")
         del q4, q4_tables, plan4
@@ -276,7 +277,8 @@ def main():
                              "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                              "weight_gbps": round(wgbs, 1), "hbm_frac": round(wgbs / HBM_PEAK_GBS, 4),
                              "attainable_tflops": round(attain, 1), "roofline_frac": round(tflops / attain, 4),
-                             "flops": fl, "weight_bytes": wb, "tokens_per_s": round(T / (pus * 1e-6), 1)}
+                             "flops": fl, "weight_bytes": wb, "tokens_per_s": round(T / (pus * 1e-6), 1),
+                             "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_prefill_t4096_h2560_e256_i1024_k8.md")}
         log(f"prefill: {pus:.1f} us/layer, {tflops:.1f} TFLOP/s, weights {wgbs:.0f} GB/s")
         del pws
 
