@@ -93,7 +93,8 @@ def main():
     ap.add_argument("--stack-tokens", type=int, default=64)
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=6)
-    ap.add_argument("--cpu-tokens", type=int, default=64)
+    ap.add_argument("--cpu-tokens", type=int, default=4096,
+                    help="decode tokens of the CPU baseline sample (~8 s of host work at the default)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-int4", action="store_true")
@@ -326,7 +327,7 @@ def main():
         gu, dn = ledger.hbm[0][0].cpu(), ledger.hbm[0][1].cpu()
         wg = ly.router_w.cpu()
         shw = tuple(t.cpu() for t in ly.shared)
-        xc = xs[0][:args.cpu_tokens].cpu()
+        xc = seeded.make_tokens(shape, 4, args.cpu_tokens, device=dev).cpu()
         for r in range(2):
             cref.moe_block(xc[r:r + 1], wg, shape.top_k, gu, dn, shape.num_experts, shw)
         times = []

@@ -235,10 +235,11 @@ __device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, in
   return (w != kUnseenWord && (int)w < p.E) ? (int)w : -1;
 }
 
-// SwiGLU of gate/up row pairs [i0, i0 + 2): one tagged activation pair.
+// SwiGLU of gate/up row pairs [i0, i0 + kPairs): kPairs / 2 tagged activation pairs.
 template <int MH, bool EXACT>
 __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* up, int i0, int n_rows, int K,
                                          const uint16_t* x, int lane, uint64_t* act64, uint32_t tag) {
+  static_assert(kPairs % 2 == 0, "activations are published as tagged bf16 pairs");
   XPack<MH> xf;
   load_xpack<MH, EXACT>(xf, x, K, lane);
   const uint16_t* rows[2 * kPairs];
@@ -250,12 +251,17 @@ __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* u
   }
   float d[2 * kPairs];
   wave_dots_p<MH, 2 * kPairs, EXACT>(rows, xf, K, lane, d);
-  static_assert(kPairs == 2, "activations are published as one tagged bf16 pair per task");
-  if (lane == 0) {
-    const uint32_t a0 = f32_to_bf16(swiglu_bf16(rbf16(d[0]), rbf16(d[2])));
-    const uint32_t a1 = (i0 + 1 < n_rows) ? f32_to_bf16(swiglu_bf16(rbf16(d[1]), rbf16(d[3]))) : 0u;
-    st64c(act64 + i0 / 2, tagged(tag, a0 | (a1 << 16)));
+  int pk[kPairs / 2];
+#pragma unroll
+  for (int h = 0; h < kPairs / 2; ++h) {
+    const int i = i0 + 2 * h;
+    const uint32_t a0 = i < n_rows ? f32_to_bf16(swiglu_bf16(rbf16(d[2 * h]), rbf16(d[kPairs + 2 * h]))) : 0u;
+    const uint32_t a1 =
+        i + 1 < n_rows ? f32_to_bf16(swiglu_bf16(rbf16(d[2 * h + 1]), rbf16(d[kPairs + 2 * h + 1]))) : 0u;
+    pk[h] = (int)(a0 | (a1 << 16));
   }
+  const uint32_t word = (uint32_t)spread(pk);
+  if (lane < kPairs / 2 && i0 + 2 * lane < n_rows) st64c(act64 + i0 / 2 + lane, tagged(tag, word));
 }
 
 // 8 rows of one down projection: d[r] = bf16(dot(w[h0 + r], act)).  The weight
