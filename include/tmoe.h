@@ -144,14 +144,18 @@ int tmoe_dequant_int4_bf16(const void* packed, const void* scales, int N, int K,
 
 /* ---------------------------------------------------------------- int4 fast mode (a10)
  * Labelled fast mode of the reference's decode (tarfa/engine/fused_int4.py:206-219 ->
- * moe_kernel.py:90-104 moe_ffn), with group-128 scales.  Batch 1 only (T == 1),
- * H and I multiples of 512.  Expert table uint64_t[E][4] (see above), entries
- * 16-byte aligned.  Per routed expert in router order: fp32 gate/up dot products
- * (int4 x bf16, fp32 accumulation, group scale applied per group), act =
- * bf16(silu(g) * u) computed in fp32, fp32 down dot products; then
- * y = y + w_j * d_j in fp32 (separately rounded products and sums), out = bf16(y).
+ * moe_kernel.py:90-104 moe_ffn), with group-128 scales.  Expert table
+ * uint64_t[E][4] (see above), entries 16-byte aligned.  Is == I or 0.
+ *   T == 1 (H and I multiples of 512): per routed expert in router order, fp32
+ *   gate/up dot products (int4 x bf16, fp32 accumulation, group scale applied per
+ *   group), act = bf16(silu(g) * u) computed in fp32, fp32 down dot products; then
+ *   y = y + w_j * d_j in fp32 (separately rounded products and sums), out = bf16(y).
+ *   T > 1 (H and I multiples of 128): the reference's int4 prefill
+ *   (fused_int4.py:247-260): each weight is dequantised to bf16((n - 8) * s), bit-exact
+ *   with tmoe_dequant_int4_bf16, inside the grouped GEMM, and the result is the exact-BF16
+ *   prefill of tmoe_experts_forward_bf16 on those dequantised weights.
  * tmoe_moe_block_int4 adds the router and the shared expert, which stays exact bf16
- * as in tmoe_moe_block_bf16: out = bf16(bf16(y) + bf16(gate * shared)).  Is == I or 0.
+ * as in tmoe_moe_block_bf16: out = bf16(bf16(y) + bf16(gate * shared)).
  * Arguments otherwise as tmoe_experts_forward_bf16 / tmoe_moe_block_bf16.
  */
 int tmoe_experts_forward_int4(const void* x, int T, const int64_t* ids, const void* weights,

@@ -14,7 +14,7 @@ int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64,
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s);
+                   void* ws, hipStream_t s, bool q4);
 int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
 }  // namespace tmoe
 
@@ -96,14 +96,15 @@ static void bind_ws(DecodeParams& p, void* ws, size_t ws_bytes, const Ws& L) {
 }
 
 
-// Int4 mode: T == 1, H and I multiples of 512 (group 128), 16-byte aligned table entries.
+// Int4 mode: group-128 scales; T == 1 needs H and I multiples of 512, T > 1 multiples of
+// 128; table entries 16-byte aligned.
 static int experts_forward(const void* x, int T, const int64_t* ids, const void* weights,
                            const uint64_t* expert_table, int H, int E, int I, int k, void* out, void* workspace,
                            size_t ws_bytes, hipStream_t s, bool q4) {
   if (int st = check_shape(T, H, E, I, k, 0)) return st;
   if (!x || !ids || !weights || !expert_table || !out || !workspace) return TMOE_ERR_NULL;
   if (misaligned(x) || misaligned(workspace)) return TMOE_ERR_ALIGN;
-  if (q4 && (T != 1 || H % 512 || I % 512)) return TMOE_ERR_SHAPE;
+  if (q4 && (T == 1 ? (H % 512 || I % 512) : (H % 128 || I % 128))) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, 0);
   if (ws_bytes < L.total) return TMOE_ERR_WORKSPACE;
   if (T == 1) {
@@ -119,7 +120,7 @@ static int experts_forward(const void* x, int T, const int64_t* ids, const void*
     return q4 ? decode_fused_launch(p, false, s) : decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
-                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s);
+                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4);
 }
 
 extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
@@ -148,7 +149,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
   if (misaligned(x) || misaligned(workspace) || (router_w && misaligned(router_w)) ||
       (has_sh && (misaligned(sh_gate) || misaligned(sh_up) || misaligned(sh_down) || misaligned(sh_gate_w))))
     return TMOE_ERR_ALIGN;
-  if (q4 && (T != 1 || H % 512 || I % 512 || (Is && Is != I))) return TMOE_ERR_SHAPE;
+  if (q4 && ((T == 1 ? (H % 512 || I % 512) : (H % 128 || I % 128)) || (Is && Is != I))) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, Is);
   if (ws_bytes < L.total) return TMOE_ERR_WORKSPACE;
   if (T == 1) {
@@ -185,7 +186,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     if (int st = launch_shared_gate((const uint16_t*)x, (const uint16_t*)sh_gate_w, T, H, gs, s)) return st;
   return prefill_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
                         (const uint16_t*)sh_up, (const uint16_t*)sh_down, has_sh ? gs : nullptr, H, E, I, k, Is,
-                        (uint16_t*)out, workspace, s);
+                        (uint16_t*)out, workspace, s, q4);
 }
 
 extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,

@@ -143,7 +143,8 @@ struct GemmParams {
   const int32_t* perm;       // [T * k]
   const int32_t* tile_start; // [n_groups + 1] cumulative M-chunks
   int T, E, k, n_groups, n_ntiles, up, N, I;
-  const uint64_t* table;     // [E][2]
+  int group_lo, group_hi;    // groups [group_lo, group_hi) of this launch
+  const uint64_t* table;     // [E][2] bf16; int4: [E][4] (packed, scales) x (gate_up, down)
   const uint16_t* shw0;      // shared: gate_proj (up) / down_proj (down)
   const uint16_t* shw1;      // shared: up_proj (up)
   int shared_row0;           // first act row of the shared group (T * k)
@@ -156,25 +157,50 @@ struct GemmParams {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// One MFMA B fragment from int4: the 8 weights of 4 packed bytes (byte b = k 2b low
+// nibble, 2b + 1 high nibble), dequantised as bf16((n - 8) * s) -- the reference's
+// `dequant_int4` then bf16 `F.linear` (tarfa/engine/fused_int4.py:258-259).  n * s - 8 s
+// is exact in fp32 (a 4-bit times an 8-bit significand), so one RNE to bf16 reproduces
+// the dequantised matrix bit for bit (finite scales).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return u + 0x7FFFu + ((u >> 16) & 1u);     // bf16 in the high half
+}
+__device__ __forceinline__ u32x4 dequant_frag(uint32_t w, float s) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  const float m8 = -8.0f * s;
+  uint32_t d[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t e = bf16_rne_bits(fmaf((float)((lo >> (8 * b)) & 0xFFu), s, m8));
+    const uint32_t o = bf16_rne_bits(fmaf((float)((hi >> (8 * b)) & 0xFFu), s, m8));
+    d[b] = __builtin_amdgcn_perm(o, e, 0x07060302u);   // (even k low, odd k high)
+  }
+  return u32x4{d[0], d[1], d[2], d[3]};
+}
+
 // Block = 4 waves; tile = (up to 256 rows of one group) x (two 16-row weight sets per
 // wave).  A is staged through LDS (double-buffered, one barrier per 64-wide K stage);
 // weights are read once, straight into MFMA B-fragment registers, kRing stages ahead.
-// RING = K stages requested ahead of the multiply.
-template <int RING>
+// RING = K stages requested ahead of the multiply; Q4: routed weights are int4 (table
+// [E][4]), dequantised into the B fragments in registers (a launch covers either the
+// routed groups in int4 or the shared group in bf16, never both).
+template <int RING, bool Q4>
 __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][kBM * kLdsStride];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
 
   // Tile index, remapped so each XCD (blocks b with equal b % 8) walks a
   // contiguous range: the N-tiles of one group share that XCD's L2 copy of A.
-  const int total = p.tile_start[p.n_groups] * p.n_ntiles;
+  const int f0 = p.tile_start[p.group_lo] * p.n_ntiles;
+  const int total = p.tile_start[p.group_hi] * p.n_ntiles - f0;
   const int per_xcd = (total + 7) / 8;
   const int q = (int)blockIdx.x >> 3, xcd = (int)blockIdx.x & 7;
   if (q >= per_xcd) return;
   const int f = xcd * per_xcd + q;
   if (f >= total) return;
-  const int mt = f / p.n_ntiles, nt = f - mt * p.n_ntiles;
-  int lo = 0, hi = p.n_groups;
+  const int mt = (f0 + f) / p.n_ntiles, nt = (f0 + f) - mt * p.n_ntiles;
+  int lo = p.group_lo, hi = p.group_hi;
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (p.tile_start[mid] <= mt) lo = mid; else hi = mid;
@@ -187,28 +213,47 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   const int m = min(kBM, gcnt - r0);
   const int K = p.K;
 
-  // Weight row sets of this wave.
-  const uint16_t *w0, *w1;
-  int c0;
+  // Weight row sets of this wave: rows r0w (first set) and r1w (second set) of the
+  // expert's gate_up [2I, K] or down [H, K] matrix, this lane's row (lane & 15) and k
+  // offset 8 (lane >> 4) within each 32-wide k step.
+  int c0, r0w, r1w;
   if (p.up) {
     c0 = nt * 64 + wid * 16;
-    if (shared) {
-      w0 = p.shw0 + (size_t)c0 * K;
-      w1 = p.shw1 + (size_t)c0 * K;
-    } else {
-      const uint16_t* gu = reinterpret_cast<const uint16_t*>(p.table[2 * g]);
-      w0 = gu + (size_t)c0 * K;
-      w1 = gu + (size_t)(p.I + c0) * K;
-    }
+    r0w = c0;
+    r1w = shared ? c0 : p.I + c0;
   } else {
     c0 = nt * 128 + wid * 32;
-    const uint16_t* dn = shared ? p.shw0 : reinterpret_cast<const uint16_t*>(p.table[2 * g + 1]);
-    w0 = dn + (size_t)c0 * K;
-    w1 = dn + (size_t)(c0 + 16) * K;
+    r0w = c0;
+    r1w = c0 + 16;
   }
-  const int bl = (lane & 15) * K + 8 * (lane >> 4);
-  const uint16_t* b0 = w0 + bl;
-  const uint16_t* b1 = w1 + bl;
+  const uint16_t *b0 = nullptr, *b1 = nullptr;      // bf16 weights
+  const uint8_t *q0 = nullptr, *q1 = nullptr;       // int4: packed rows (K / 2 bytes) ...
+  const uint16_t *s0 = nullptr, *s1 = nullptr;      // ... and their group scales (K / 128)
+  if (Q4) {
+    const int part = p.up ? 0 : 2;
+    const uint8_t* pk = reinterpret_cast<const uint8_t*>(p.table[4 * g + part]);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(p.table[4 * g + part + 1]);
+    const int row = lane & 15;
+    q0 = pk + (size_t)(r0w + row) * (K / 2) + 4 * (lane >> 4);
+    q1 = pk + (size_t)(r1w + row) * (K / 2) + 4 * (lane >> 4);
+    s0 = sc + (size_t)(r0w + row) * (K / 128);
+    s1 = sc + (size_t)(r1w + row) * (K / 128);
+  } else {
+    const uint16_t *w0, *w1;
+    if (p.up) {
+      if (shared) {
+        w0 = p.shw0;
+        w1 = p.shw1;
+      } else {
+        w0 = w1 = reinterpret_cast<const uint16_t*>(p.table[2 * g]);
+      }
+    } else {
+      w0 = w1 = shared ? p.shw0 : reinterpret_cast<const uint16_t*>(p.table[2 * g + 1]);
+    }
+    const int bl = (lane & 15) * K + 8 * (lane >> 4);
+    b0 = w0 + (size_t)r0w * K + bl;
+    b1 = w1 + (size_t)r1w * K + bl;
+  }
 
   // A rows this thread stages: rows tid/8 + 32 i, 16-byte column chunk tid % 8.  Rows past
   // the group repeat its last row, so every load is unconditional (results of those rows
@@ -237,6 +282,7 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   // straight from registers into the MFMA.  Ring slots are static (the loop is unrolled
   // by RING).
   u32x4 areg[RING][kAS], breg[RING][2][2];
+  uint32_t qreg[RING][2][2], sreg[RING][2];           // int4: packed words and scales in flight
   const int nk = K / kBK;
   auto load_a = [&](int slot, int st) {
     const int k0 = st * kBK;
@@ -245,10 +291,21 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   };
   auto load_b = [&](int slot, int st) {
     const int k0 = st * kBK;
+    if constexpr (Q4) {
+      // A 64-wide stage lies inside one 128-column scale group.
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      breg[slot][ks][0] = ld_stream(b0 + k0 + 32 * ks);
-      breg[slot][ks][1] = ld_stream(b1 + k0 + 32 * ks);
+      for (int ks = 0; ks < 2; ++ks) {
+        qreg[slot][ks][0] = ld_stream4(q0 + (k0 + 32 * ks) / 2);
+        qreg[slot][ks][1] = ld_stream4(q1 + (k0 + 32 * ks) / 2);
+      }
+      sreg[slot][0] = s0[k0 / 128];
+      sreg[slot][1] = s1[k0 / 128];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        breg[slot][ks][0] = ld_stream(b0 + k0 + 32 * ks);
+        breg[slot][ks][1] = ld_stream(b1 + k0 + 32 * ks);
+      }
     }
   };
   auto store_a = [&](int buf, int slot) {
@@ -264,7 +321,14 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   auto multiply = [&](int buf, int slot) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8_t bg = as_bf16x8(breg[slot][ks][0]), bu = as_bf16x8(breg[slot][ks][1]);
+      bf16x8_t bg, bu;
+      if constexpr (Q4) {
+        bg = as_bf16x8(dequant_frag(qreg[slot][ks][0], bf16_to_f32((uint16_t)sreg[slot][0])));
+        bu = as_bf16x8(dequant_frag(qreg[slot][ks][1], bf16_to_f32((uint16_t)sreg[slot][1])));
+      } else {
+        bg = as_bf16x8(breg[slot][ks][0]);
+        bu = as_bf16x8(breg[slot][ks][1]);
+      }
       u32x4 av[kSubs];
 #pragma unroll
       for (int sub = 0; sub < kSubs; ++sub)
@@ -420,9 +484,10 @@ int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, in
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s) {
+                   void* ws, hipStream_t s, bool q4) {
   const bool has_sh = sh_gate != nullptr;
   if (H % 128 || I % 64 || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
+  if (q4 && I % 128) return TMOE_ERR_SHAPE;   // int4: every 64-wide K stage inside one 128-column group
   const Ws L = ws_layout(T, H, E, I, k, Is);
   int32_t* offsets = ws_ptr<int32_t>(ws, L.offsets);
   int32_t* perm = ws_ptr<int32_t>(ws, L.perm);
@@ -437,19 +502,35 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
 
   const int n_groups = has_sh ? E + 1 : E;
   const long mbound = (long)T * k / kBM + (long)(E < T * k ? E : T * k) + (has_sh ? (T + kBM - 1) / kBM : 0) + 1;
+  const long mshared = (T + kBM - 1) / kBM;
 
+  // One GEMM over groups [lo, hi): bf16 weights, or int4 routed weights (the shared
+  // group, always bf16, then gets a launch of its own).
+  auto gemm = [&](GemmParams g, int lo, int hi, bool routed_q4, long mchunks) {
+    g.group_lo = lo;
+    g.group_hi = hi;
+    const long grid = (mchunks * g.n_ntiles + 7) / 8 * 8;
+    if (routed_q4)
+      hipLaunchKernelGGL((k_grouped_gemm<kRing, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((k_grouped_gemm<kRing, false>), dim3((unsigned)grid), dim3(256), 0, s, g);
+  };
   GemmParams up{};
   up.a = x; up.K = H; up.gather = 1; up.offsets = offsets; up.perm = perm; up.tile_start = tile_start;
   up.T = T; up.E = E; up.k = k; up.n_groups = n_groups; up.n_ntiles = I / 64; up.up = 1; up.N = I; up.I = I;
   up.table = table; up.shw0 = sh_gate; up.shw1 = sh_up; up.shared_row0 = T * k; up.out = act;
-  long gu = (mbound * up.n_ntiles + 7) / 8 * 8;
-  hipLaunchKernelGGL(k_grouped_gemm<kRing>, dim3((unsigned)gu), dim3(256), 0, s, up);
-
   GemmParams dn = up;
   dn.a = act; dn.K = I; dn.gather = 0; dn.n_ntiles = H / 128; dn.up = 0; dn.N = H;
   dn.shw0 = sh_down; dn.shw1 = nullptr; dn.out = ch; dn.out_sh = sh; dn.wf = wf; dn.wb = wb; dn.gs = gs;
-  long gd = (mbound * dn.n_ntiles + 7) / 8 * 8;
-  hipLaunchKernelGGL(k_grouped_gemm<kRing>, dim3((unsigned)gd), dim3(256), 0, s, dn);
+  if (q4) {
+    gemm(up, 0, E, true, mbound);
+    if (has_sh) gemm(up, E, E + 1, false, mshared);
+    gemm(dn, 0, E, true, mbound);
+    if (has_sh) gemm(dn, E, E + 1, false, mshared);
+  } else {
+    gemm(up, 0, n_groups, false, mbound);
+    gemm(dn, 0, n_groups, false, mbound);
+  }
 
   const int nc = (H + 511) / 512;
   const dim3 gc((T + 3) / 4), bc(256);

@@ -44,6 +44,9 @@ __device__ __forceinline__ u32x4 ld_stream(const void* p) {
   return __builtin_nontemporal_load((g_u32x4*)p);
 }
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(g_u32x4*)p; }
+__device__ __forceinline__ uint32_t ld_stream4(const void* p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint32_t*)p);
+}
 
 // Dot of 8 bf16 weights (packed in 4 dwords) with 8 fp32 activations.
 __device__ __forceinline__ float dot8(const u32x4 w, const float* x, float acc) {

@@ -65,8 +65,4 @@ __device__ __forceinline__ float q4_scale(uint32_t sreg, int dw, uint32_t sel) {
   return __uint_as_float(__builtin_amdgcn_perm(0u, v, sel));
 }
 
-__device__ __forceinline__ uint32_t ld_stream4(const void* p) {
-  return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint32_t*)p);
-}
-
 }  // namespace tmoe

@@ -55,12 +55,12 @@ def test_entry_points_reject_bad_arguments_without_touching_the_device():
     assert lib.tmoe_router_topk(None, None, None, 1, 2560, 256, 17, None, None, None, None, None) == -2
     assert lib.tmoe_dispatch(None, 4, 8, 256, None, None, None, None, 0, None) == -1
     assert lib.tmoe_fill_bf16(None, 16, 1, 1.0, 0, None) == -1
-    # int4 entry points: NULLs and unsupported shapes (T > 1, H or I not a multiple of 512, bad group)
+    # int4 entry points: NULLs and unsupported shapes (decode: H, I multiples of 512; prefill: of 128)
     assert lib.tmoe_experts_forward_int4(None, 1, None, None, None, 2560, 256, 1024, 8, None, None, 0, None) == -1
     assert lib.tmoe_moe_block_int4(None, 1, None, None, None, None, None, None, None, 2560, 256, 1024, 8, 0,
                                    None, None, None, None, None, 0, None) == -1
     p = 256   # any non-NULL, 16-byte aligned value: rejected before it is dereferenced
-    assert lib.tmoe_experts_forward_int4(p, 2, p, p, p, 2560, 256, 1024, 8, p, p, 1 << 30, None) == -2
+    assert lib.tmoe_experts_forward_int4(p, 2, p, p, p, 2560, 256, 960, 8, p, p, 1 << 30, None) == -2  # I % 128
     assert lib.tmoe_experts_forward_int4(p, 1, p, p, p, 2304, 256, 1024, 8, p, p, 1 << 30, None) == -2
     assert lib.tmoe_moe_block_int4(p, 1, p, None, p, p, p, p, p, 2560, 256, 1024, 8, 512,
                                    p, None, None, None, p, 1 << 30, None) == -2        # Is != I

@@ -210,3 +210,35 @@ def test_int4_and_bf16_calls_share_a_workspace(gpu):
         assert torch.equal(tm.moe_block(shape, x, t16, ws, router_w=layer.router_w)[0], a16)
         assert torch.equal(tm.moe_block(shape, x, t4, ws, router_w=layer.router_w)[0], a4)
     ws.status()
+
+
+@pytest.mark.parametrize("T,shared", [(37, True), (300, False), (2, True)])
+def test_int4_prefill_matches_dequantised_bf16_chain(gpu, T, shared):
+    """T > 1 in int4 mode: the reference dequantises each hit expert and runs the bf16 prefill
+    chain on it (tarfa/engine/fused_int4.py:249-261), so the oracle is experts_prefill on the
+    dequantised weights, combined in ascending expert id; the shared expert stays bf16."""
+    shape = MoEShape(1024, 32, 512, 8, 512 if shared else 0)
+    layer = seeded.make_layer(shape, 40 + T, device=gpu)
+    q4 = _q4_layer(layer)
+    table = tm.expert_table_q4(*q4)
+    ws = Workspace(shape, gpu, tokens=T)
+    x = seeded.make_tokens(shape, 40 + T, T, device=gpu)
+    out, ids, w = tm.moe_block(shape, x, table, ws, router_w=layer.router_w, shared=layer.shared)
+    torch.cuda.synchronize()
+    lg = moe.router_logits(f32(x), f32(layer.router_w))
+    ids_ref, w_ref, _ = moe.router_topk(lg, shape.top_k)
+    gaps = moe.topk_gaps(lg, shape.top_k)
+    clear = gaps > 1e-5 * np.maximum(1.0, np.abs(lg).max(axis=-1))
+    assert np.array_equal(ids.cpu().numpy()[clear], ids_ref[clear])
+    gq, gs, dq, ds = q4
+    gu = {e: bf16.to_f32(int4.dequant(gq[e].cpu().numpy(), u16(gs[e]))) for e in range(shape.num_experts)}
+    dn = {e: bf16.to_f32(int4.dequant(dq[e].cpu().numpy(), u16(ds[e]))) for e in range(shape.num_experts)}
+    ids_d, w_d = ids.cpu().numpy(), f32(w)          # the device routing (ties near fp32 noise resolved alike)
+    ref = moe.experts_prefill(f32(x), ids_d, w_d, gu, dn, shape.num_experts)
+    if shared:
+        ref = moe.add_bf16(ref, moe.shared_expert(f32(x), *[f32(t) for t in layer.shared]))
+    assert_close_bf16(f32(out), ref, f"int4 prefill T={T}")
+    # experts.forward boundary with the same routing
+    out2 = tm.experts_forward(shape, x, ids, w, table, ws)
+    assert_close_bf16(f32(out2), moe.experts_prefill(f32(x), ids_d, w_d, gu, dn, shape.num_experts), "int4 experts")
+    ws.status()
