@@ -239,6 +239,40 @@ def main():
                           "traffic": profiled_traffic("k_decode_fused_int4_decode_h2560_e256_i1024_k8.md"),
                           "steps": K4, "tokens_per_s_48_layers": round(1e6 / (48 * us4), 2)}
         log(f"int4 decode: {us4:.2f} us/token-layer, {gbs4:.0f} GB/s")
+        if not args.no_prefill:
+            # int4 prefill: T=4096, logits supplied; weights dequantised into the MFMA fragments
+            T4, P4 = 4096, args.prefill_steps
+            pws4 = Workspace(shape, dev, tokens=T4)
+            px4 = seeded.make_tokens(shape, 2, T4, device=dev)
+            plg4 = [seeded.make_logits(shape, 2, T4, layer=l, device=dev) for l in range(min(L, P4 + 1))]
+            pout4 = torch.empty(T4, H, dtype=torch.bfloat16, device=dev)
+            pi4 = torch.empty(T4, shape.top_k, dtype=torch.int64, device=dev)
+            pw4 = torch.empty(T4, shape.top_k, dtype=torch.bfloat16, device=dev)
+
+            def prefill4(i):
+                l = i % len(plg4)
+                tm.moe_block(shape, px4, q4_tables[l], pws4, logits=plg4[l], shared=layers[l].shared, out=pout4,
+                             ids=pi4, weights=pw4)
+
+            prefill4(0)
+            torch.cuda.synchronize()
+            e0.record()
+            for i in range(1, P4 + 1):
+                prefill4(i)
+            e1.record()
+            torch.cuda.synchronize()
+            pws4.status()
+            pus4 = e0.elapsed_time(e1) * 1e3 / P4
+            # routed: 3*H*I nibbles + one bf16 scale per 128 columns per expert; shared expert bf16
+            wb4 = shape.num_experts * 3 * H * shape.intermediate * (64 + 2) // 128 + \
+                2 * 3 * H * shape.shared_intermediate
+            result["int4"]["prefill"] = {
+                "workload": "int4 prefill chunk T=4096 through one full-size layer (logits ~N(0,1) supplied, shared "
+                            "expert bf16): routed weights dequantised in registers into the MFMA fragments",
+                "us_per_layer": round(pus4, 1), "tflops": round(prefill_flops(shape, T4) / (pus4 * 1e-6) / 1e12, 1),
+                "weight_bytes": wb4, "weight_gbps": round(wb4 / (pus4 * 1e-6) / 1e9, 1)}
+            log(f"int4 prefill: {pus4:.1f} us/layer")
+            del pws4, px4, plg4
         del q4, q4_tables, plan4
 
     # ---------------- prefill: T = 4096 through the same layer shape, logits supplied

@@ -41,10 +41,15 @@
 //     of its waves at a time polls memory, so every block asks memory once.
 //   - Queue q (of 32) is served by wave q % 4 of the blocks b with b % 8 == q / 4
 //     (one XCD) and holds tasks q, q + 32, ...; the wave of rank r = b / 8 among
-//     its queue's `users` takes tickets r, r + users, r + 2 users, ...  Each wave
-//     runs its tasks in increasing order, a task only waits on tasks with smaller
-//     indices, and the grid fits on the GPU at once, so the smallest unfinished
-//     task is always some running wave's current task and can finish.
+//     its queue's `users` takes ticket r first.  In exact-bf16 mode every later
+//     ticket is drawn from the queue's counter (users + draw), so tasks start in
+//     list order; the draw for the next task is issued when a task starts and read
+//     after the task's loads, before its stores (gfx9 counts stores in vmcnt, and
+//     vector memory returns in issue order).  In int4 mode the tickets are static:
+//     r + users, r + 2 users, ...  Either way tickets of a queue are taken in
+//     increasing order, a task only waits on tasks with smaller indices, and the
+//     grid fits on the GPU at once, so the smallest unfinished task is always some
+//     running wave's current or next task and can finish.
 //   - Every poll backs off and is bounded (kErrTimeout on expiry).
 //   - The last wave to leave a queue re-zeroes its exit count; the last queue to
 //     drain advances the epoch.
@@ -68,6 +73,12 @@ constexpr int q4_down_rows(int MI) { return MI <= 2 ? 16 : 8; }
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
+// Tickets after a wave's first: drawn from a per-queue counter (tasks then start
+// in list order; exact-bf16 mode) or static (rank + users * i; int4 mode, where
+// waves that reach down tasks early keep their weight loads in flight while the
+// gate/up tasks finish).
+template <bool Q4>
+constexpr bool dynamic_tickets() { return !Q4; }
 constexpr int kBlocksPerCU = 2;        // resident blocks per CU (bounds the bytes in flight per XCD)
 constexpr uint32_t kSpinLimit = 1u << 20;   // polls, each >= 64 cycles apart: never reached by a healthy graph
 static_assert(kQueues == 8 * kWaves, "queue q is served by wave q % 4 of the blocks b with b % 8 == q / 4");
@@ -236,9 +247,9 @@ __device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, in
 }
 
 // SwiGLU of gate/up row pairs [i0, i0 + kPairs): kPairs / 2 tagged activation pairs.
-template <int MH, bool EXACT>
+template <int MH, bool EXACT, typename Take>
 __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* up, int i0, int n_rows, int K,
-                                         const uint16_t* x, int lane, uint64_t* act64, uint32_t tag) {
+                                         const uint16_t* x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
   static_assert(kPairs % 2 == 0, "activations are published as tagged bf16 pairs");
   XPack<MH> xf;
   load_xpack<MH, EXACT>(xf, x, K, lane);
@@ -261,6 +272,7 @@ __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* u
     pk[h] = (int)(a0 | (a1 << 16));
   }
   const uint32_t word = (uint32_t)spread(pk);
+  take();
   if (lane < kPairs / 2 && i0 + 2 * lane < n_rows) st64c(act64 + i0 / 2 + lane, tagged(tag, word));
 }
 
@@ -294,9 +306,9 @@ __device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act
 // [2I, H/2], scales [2I, H/128]): fp32 gate and up values (no rounding), then
 // act = bf16(silu(g) * u) in fp32 (tarfa/engine/moe_kernel.py:100), published as R/2
 // tagged bf16 pairs.  Loads in need order: input, scales, then the 2R weight rows.
-template <int MH, int R>
+template <int MH, int R, typename Take>
 __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int i0, int I, int H,
-                                      const uint16_t* x, int lane, uint64_t* act64, uint32_t tag) {
+                                      const uint16_t* x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
   constexpr int G = 4 * MH;            // scale groups per row (H = 512 MH)
   constexpr int NW = R * G / 2;        // scale words of R rows
   static_assert(R % 2 == 0 && NW <= 128, "scale words of a block fit two per lane");
@@ -343,6 +355,7 @@ __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int
     pk[h] = (int)(a0 | (a1 << 16));
   }
   const uint32_t word = (uint32_t)spread(pk);
+  take();
   if (lane < R / 2) st64c(act64 + i0 / 2 + lane, tagged(tag, word));
 }
 
@@ -502,8 +515,9 @@ __device__ __forceinline__ void top8_bitonic(const float (&v)[4], int E, int k, 
 // Kept compact (rolled rounds, per-slot values held by lane r): this runs once
 // per call on a cold instruction cache while the rest of the GPU streams, so code
 // size is latency here.
-template <int MAXEPL>
-__device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane, uint32_t tag, uint32_t* err) {
+template <int MAXEPL, typename Take>
+__device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane, uint32_t tag, uint32_t* err,
+                                                Take&& take) {
   const bool has_sh = p.sh_gate != nullptr;
   __builtin_amdgcn_s_setprio(3);   // the routing gates every expert task: issue ahead of streaming waves
   float v[MAXEPL];
@@ -538,6 +552,7 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
       if (!b.step(err)) break;
     }
   }
+  take();
   int my_id = p.E;          // lane r < k: slot r's expert and logit
   float my_lw = -INFINITY;
   float m = 0.f;            // the largest logit (slot 0)
@@ -635,8 +650,8 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
 }
 
 // Router rows [4t, 4t + 4) of E + 1 (row E: the shared-gate weight).
-template <int MH, bool EXACT>
-__device__ __forceinline__ void task_router(const DecodeParams& p, int t, int lane, uint32_t tag) {
+template <int MH, bool EXACT, typename Take>
+__device__ __forceinline__ void task_router(const DecodeParams& p, int t, int lane, uint32_t tag, Take&& take) {
   const int n_lrows = p.logits_in ? 0 : p.E;
   const int n_rows = n_lrows + (p.sh_gate ? 1 : 0);
   const int r0 = t * kRouterRows;
@@ -651,6 +666,7 @@ __device__ __forceinline__ void task_router(const DecodeParams& p, int t, int la
   }
   float d[kRouterRows];
   wave_dots_p<MH, kRouterRows, EXACT>(rp, xf, p.H, lane, d);
+  take();
   if (lane < kRouterRows && r0 + lane < n_rows) {
     float v = d[0];
 #pragma unroll
@@ -788,9 +804,9 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
 
 // Int4 mode, a D task of routed slot j: RQ rows published as one fp32 word each (a
 // skipped slot publishes zeros the combine ignores), or combined for the last slot.
-template <int MI, int RQ>
+template <int MI, int RQ, typename Take>
 __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, int idx, int lane, uint32_t& rwc,
-                                             uint32_t tag, uint32_t* err, RouteLds& L) {
+                                             uint32_t tag, uint32_t* err, RouteLds& L, Take&& take) {
   const int e = wave_slot_expert(p, slot, lane, rwc, tag, err, L);
   const int h0 = idx * RQ;
   float d[RQ];
@@ -800,6 +816,7 @@ __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, in
     down_q4<MI, RQ>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 3)), p.act64 + (size_t)slot * p.I / 2,
                     p.I, h0, lane, d, tag, err);
+  if (e >= 0) take();
   if (slot != p.k - 1) {
     int rows[RQ];
 #pragma unroll
@@ -895,23 +912,45 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       rwc = p.w_in[lane0 - kRwW];
     }
   }
+  constexpr bool DYN = dynamic_tickets<Q4>();
+  uint32_t* draw = line(p, kLnQueueExit + q) + kQueueDrawWord;
+  uint32_t ticket = rank;
   for (uint32_t i = 0;; ++i) {
-    // Tickets rank, rank + users, ... of queue q: no atomic between tasks (a wait
-    // on a draw would also wait for this wave's stores, which gfx9 counts in vmcnt).
-    const int t = q + kQueues * (int)(rank + users * i);
+    const int t = q + kQueues * (int)ticket;
     if (t >= p.n_tasks) break;
+    // The next ticket: drawn now from the queue's counter (first tickets are the
+    // ranks), read after this task.  Vector memory returns in issue order, so the
+    // task's own loads bring the draw back with them.
+    uint32_t nxt = 0, nt = 0;
+    bool got = !DYN;
+    // Each task reads the drawn ticket right after its loads and before its stores
+    // (a read after the stores would wait for them: gfx9 counts stores in vmcnt).
+    auto take = [&]() {
+      if (!got) {
+        nt = (uint32_t)__builtin_amdgcn_readlane((int)nxt, 0);
+        got = true;
+      }
+    };
+    if (DYN && lane0 == 0) {
+      // An opaque (per-lane) address keeps this one lane's atomic as it is: the
+      // compiler's wave-aggregated form broadcasts the result at once, waiting for it.
+      uintptr_t a = reinterpret_cast<uintptr_t>(draw);
+      asm volatile("" : "+v"(a));
+      nxt = __hip_atomic_fetch_add(reinterpret_cast<__attribute__((address_space(1))) uint32_t*>(a), 1u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // The lane index is re-derived per task: otherwise every per-lane address of
     // every task type is hoisted out of this loop and held in registers throughout.
     int lane = lane0;
     asm volatile("" : "+v"(lane));
     const TaskRef tk = decode_task(p, t);
     if (tk.type == kTR) {
-      task_router<MH, EXACT>(p, tk.idx, lane, tag);
+      task_router<MH, EXACT>(p, tk.idx, lane, tag, take);
     } else if (tk.type == kTK) {
       if (p.E <= 256)
-        resolve_routing<4>(p, lane, tag, err);
+        resolve_routing<4>(p, lane, tag, err, take);
       else
-        resolve_routing<16>(p, lane, tag, err);
+        resolve_routing<16>(p, lane, tag, err, take);
     } else if (tk.type == kTS || tk.type == kTG) {
       // Gate/up pairs: the shared expert (S) or routed slot j (G); one call site.
       const bool shared = tk.type == kTS;
@@ -921,16 +960,16 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         if (e >= 0)
           up_q4<MH, kQ4Pairs>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 1)), tk.idx * kQ4Pairs, p.I, p.H,
-                    p.x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag);
+                    p.x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag, take);
       } else if (e >= 0) {
         const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
         const uint16_t* g = shared ? p.sh_gate : gu;
         const uint16_t* u = shared ? p.sh_up : gu + (size_t)p.I * p.H;
         up_pairs<MH, EXACT>(g, u, tk.idx * kPairs, n_rows, p.H, p.x, lane,
-                            p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag);
+                            p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag, take);
       }
     } else if (Q4 && tk.type == kTD) {
-      task_down_q4<MI, RQ>(p, tk.slot, tk.idx, lane, rwc, tag, err, s_rt);
+      task_down_q4<MI, RQ>(p, tk.slot, tk.idx, lane, rwc, tag, err, s_rt, take);
     } else {
       // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
@@ -941,6 +980,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         const uint16_t* w = shared ? p.sh_down : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e + 1));
         const uint64_t* a = p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2);
         down_dots<MI, EXACT>(w, a, p, shared ? p.Is : p.I, h0, lane, d, tag, err);
+        take();
       }
       if (Q4) {
         // Int4 mode keeps one row per word: the shared rows as fp32 words of their bf16 values.
@@ -963,6 +1003,13 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         combine_rows(p, e, h0, lane, d, rwc, tag, err, s_rt);
       }
     }
+    if (!got) {
+      // A task that loaded nothing (skipped slot): the draw is read here.
+      uint32_t v = nxt;
+      asm volatile("" : "+v"(v));
+      nt = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    }
+    ticket = DYN ? users + nt : rank + users * (i + 1);
   }
   // The last wave to leave queue q re-zeroes its exit count; the last queue to
   // drain ends the call.
@@ -970,6 +1017,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   if (lane0 == 0) {
     if (add32c(line(p, kLnQueueExit + q), 1u) == users - 1u) {
       st32c(line(p, kLnQueueExit + q), 0u);
+      st32c(draw, 0u);
       fin = add32c(line(p, kLnQueuesDone), 1u) == (uint32_t)kQueues - 1u;
     }
   }

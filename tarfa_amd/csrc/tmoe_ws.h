@@ -36,6 +36,8 @@ enum SyncLine {
 // Each queue line also carries a copy of the epoch, read by that queue's waves
 // (coherent loads of one line serialise, so 2048 waves must not share one word).
 constexpr int kQueueEpochWord = 16;
+// Each queue's exit line also holds its ticket counter (drawn once per task).
+constexpr int kQueueDrawWord = 32;
 // u64 words {payload, tag} of a route replica line: the expert ids of slots 0..7,
 // their bf16 weights, the shared-expert bf16 gate.  Ids are published first.
 enum RouteWord { kRwId = 0, kRwW = 8, kRwGate = 16, kRouteWords = 17 };
