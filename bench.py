@@ -53,12 +53,12 @@ def prefill_weight_bytes(s):
     return 2 * (E * 3 * H * I + 3 * H * Is)
 
 
-def profiled_traffic(name):
+def profiled_traffic(name, key="traffic_bytes_per_launch"):
     """HBM bytes per launch recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes in profiles/<name>."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return int(float(line.split(":", 1)[1]))
     except OSError:
         pass
@@ -270,7 +270,9 @@ def main():
                 "workload": "int4 prefill chunk T=4096 through one full-size layer (logits ~N(0,1) supplied, shared "
                             "expert bf16): routed weights dequantised in registers into the MFMA fragments",
                 "us_per_layer": round(pus4, 1), "tflops": round(prefill_flops(shape, T4) / (pus4 * 1e-6) / 1e12, 1),
-                "weight_bytes": wb4, "weight_gbps": round(wb4 / (pus4 * 1e-6) / 1e9, 1)}
+                "weight_bytes": wb4, "weight_gbps": round(wb4 / (pus4 * 1e-6) / 1e9, 1),
+                "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_prefill_t4096_h2560_e256_i1024_k8.md",
+                                                            "int4_traffic_bytes_per_launch")}
             log(f"int4 prefill: {pus4:.1f} us/layer")
             del pws4, px4, plg4
         del q4, q4_tables, plan4
