@@ -89,7 +89,8 @@ static void bind_ws(DecodeParams& p, void* ws, size_t ws_bytes, const Ws& L) {
   p.sh_ws = ws_ptr<uint16_t>(ws, L.sh);
   p.sync = ws_ptr<uint32_t>(ws, L.sync);
   p.lg64 = ws_ptr<uint64_t>(ws, L.tagged);
-  p.act64 = p.lg64 + (p.E + 1);
+  p.lg_stride = logit_stride(p.E);
+  p.act64 = p.lg64 + (size_t)kLogitReplicas * p.lg_stride;
   p.dq64 = p.act64 + ((size_t)p.k * p.I + p.Is) / 2;
   p.handoff = ws_ptr<void>(ws, L.logits);
   p.handoff_words = (ws_bytes - L.logits) / 8;

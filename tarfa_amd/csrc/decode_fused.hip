@@ -2,11 +2,11 @@
 // 32 dependency-ordered queues.
 //
 // Tasks (each one wave), in list order:
-//   R   router rows: fp32 logits, 4 rows per task (row E = the shared-gate logit)
-//   K   gather every logit, top-k, publish the routing   (needs: all R)
+//   R   router rows: fp32 logits, 4 rows per task (row E = the shared-gate logit),
+//       each written to all kLogitReplicas copies of the logits
 //   S   shared expert gate/up, 2 row pairs -> 2 bf16 SwiGLU activations
 //   SD  shared expert down, 8 rows                     (needs: every S)
-//   Gj  routed gate/up of slot j, 2 row pairs          (needs: slot j's expert id)
+//   Gj  routed gate/up of slot j, 2 row pairs          (needs: the routing)
 //   Dj  routed down of slot j, 8 rows                  (needs: every Gj)
 //       D(k-1), last in the list, also combines its rows from every slot's tagged
 //       results: acc = bf16(acc + bf16(w_j * d_j)) in router order, then
@@ -16,18 +16,21 @@
 // 16 rows (8 when I > 1024) with fp32 results, and the combine is the fp32 sum
 // y = y + w_j * d_j in router order, cast to bf16 once, plus the bf16 shared expert
 // (tarfa/engine/moe_kernel.py:90-104, fused_int4.py:206-219).
-// ordered R, K, G0 .. G(L), then D(j-L) after each later Gj (L = kDownLag), S
+// The list is ordered R, G0 .. G(L), then D(j-L) after each later Gj (L = kDownLag), S
 // after G(kSharedAfter) and SD L slots later, then the remaining D: while the
-// routing resolves only the router rows load, and down rows are drawn only once
-// their gate/up tasks have had time to finish.  K keeps its vector-memory
-// instructions few (a wave's store waits behind every load queued on its CU):
-// 5 loads, then the whole routing in 3 stores.
+// routing resolves only the router rows and the shared expert load, and down rows
+// are drawn only once their gate/up tasks have had time to finish.
+// The routing (top-k, softmax weights, shared gate) is resolved in every block: the
+// first of its waves to need it polls the block's copy of the logits (32 copies, so
+// 16 blocks read each), selects and writes the route words to LDS for the block.  A
+// single resolving task would add a publish and a second poll through memory to the
+// critical path.
 //
 // Hand-offs are built around measured MI355X costs: a memory round trip under
 // streaming load is several us, atomics on one hot 256-B line serialise at ~11 ns,
 // and every poll of a coherent word travels to the memory side like the weight
 // stream itself, so polling must be cheap.
-//   - Logits, routing, activations and per-slot down rows travel as TAGGED 64-bit
+//   - Logits, activations and per-slot down rows travel as TAGGED 64-bit
 //     words {payload, tag}: one device-coherent store (relaxed agent-scope atomics
 //     bypass the per-XCD L2 copies), so a consumer checks the data itself -- no
 //     store-completion wait, no cache-wide write-back / invalidate.
@@ -37,8 +40,7 @@
 //   - A down task reads its activations with plain loads issued together with its
 //     weight rows (queued kDownLag slots after its gate/up tasks, the activations
 //     are normally complete); stale words are re-polled with coherent loads.
-//   - Each wave caches the routing it has seen; a block keeps a copy in LDS and one
-//     of its waves at a time polls memory, so every block asks memory once.
+//   - Each wave caches the routing; the block's copy in LDS is resolved once.
 //   - Queue q (of 32) is served by wave q % 4 of the blocks b with b % 8 == q / 4
 //     (one XCD) and holds tasks q, q + 32, ...; the wave of rank r = b / 8 among
 //     its queue's `users` takes ticket r first.  In exact-bf16 mode every later
@@ -83,7 +85,7 @@ constexpr int kBlocksPerCU = 2;        // resident blocks per CU (bounds the byt
 constexpr uint32_t kSpinLimit = 1u << 20;   // polls, each >= 64 cycles apart: never reached by a healthy graph
 static_assert(kQueues == 8 * kWaves, "queue q is served by wave q % 4 of the blocks b with b % 8 == q / 4");
 
-enum TaskType { kTR, kTK, kTS, kTSD, kTG, kTD };
+enum TaskType { kTR = 0, kTS = 2, kTSD = 3, kTG = 4, kTD = 5 };
 
 __device__ __forceinline__ uint32_t ld32c(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -96,6 +98,15 @@ __device__ __forceinline__ uint64_t ld64c(const uint64_t* p) {
 }
 __device__ __forceinline__ void st64c(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Two consecutive tagged words in one 16-byte vector store (p 16-byte aligned) with the
+// cache policy of st64c's agent-scope store (sc1); each word carries its own tag, so the
+// pair needs no atomicity.  (Issued from inline assembly, the store is not in the
+// compiler's count of outstanding vector-memory operations; that can only make its later
+// waits stricter.)
+__device__ __forceinline__ void st128c(uint64_t* p, uint64_t a, uint64_t b) {
+  const u32x4 v = {(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ uint32_t add32c(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -179,72 +190,14 @@ __device__ __forceinline__ void load_acts(XPack<MAXC>& f, const uint64_t* w, int
   }
 }
 
-__device__ __forceinline__ uint64_t* route_line(const DecodeParams& p, int r) {
-  return line64(p, kLnRoute + r * kRouteStride);
-}
-
-// Routing as seen by one block: the route words (lane layout of RouteWord) and a
-// mask of those known; one wave at a time polls memory for the block.
+// Routing as seen by one block: the route words (lane layout of RouteWord), set once
+// (valid) by the block's resolving wave (poller).
 struct RouteLds {
   uint32_t word[kRouteWords];
   uint32_t valid;
   uint32_t poller;
 };
-
-// The wave's routing cache `rwc` (lane l < kRouteWords holds route word l once
-// seen, kUnseenWord before) is completed until every lane in `need` is seen:
-// from the block's copy in LDS, else by becoming the block's poller.
 constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
-
-__device__ __forceinline__ void route_fetch(const DecodeParams& p, int lane, uint32_t& rwc, uint32_t need, uint32_t tag,
-                                         uint32_t* err, RouteLds& L) {
-  const uint64_t* rt = route_line(p, (int)(blockIdx.x % kRouteReplicas));
-  const bool has_sh = p.sh_gate != nullptr;
-  const bool used = lane < p.k || (lane >= kRwW && lane < kRwW + p.k) || (lane == kRwGate && has_sh);
-  Backoff<16> b;
-  for (;;) {
-    const uint32_t valid = __hip_atomic_load(&L.valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if ((valid & need) == need) {
-      if (lane < kRouteWords && ((valid >> lane) & 1u)) rwc = L.word[lane];
-      return;
-    }
-    uint32_t got = 0;
-    if (lane == 0) got = atomicCAS(&L.poller, 0u, 1u) == 0u;
-    if (__builtin_amdgcn_readfirstlane(got)) {
-      // This wave polls the block's replica until the words in `need` are published.
-      for (;;) {
-        uint64_t w = 0;
-        if (used) w = ld64c(rt + lane);
-        const bool now = used && has_tag(w, tag);
-        const uint32_t nv = (uint32_t)__ballot(now);
-        if (now) L.word[lane] = (uint32_t)w;
-        __threadfence_block();
-        if (lane == 0) atomicOr(&L.valid, nv);
-        if ((nv & need) == need) break;
-        if (!b.step(err)) break;
-      }
-      if (lane == 0) atomicExch(&L.poller, 0u);
-      const uint32_t v2 = __hip_atomic_load(&L.valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (lane < kRouteWords && ((v2 >> lane) & 1u)) rwc = L.word[lane];
-      return;
-    }
-    if (!b.step(err)) return;
-  }
-}
-
-__device__ __forceinline__ void route_need(const DecodeParams& p, int lane, uint32_t& rwc, uint32_t need, uint32_t tag,
-                                           uint32_t* err, RouteLds& L) {
-  if ((uint32_t)__ballot(rwc == kUnseenWord) & need) route_fetch(p, lane, rwc, need, tag, err, L);
-}
-
-// Expert of slot j (wave-uniform) for this wave, or -1 for a skipped or invalid id
-// (caller-supplied routing is in the cache from the start).
-__device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, int lane, uint32_t& rwc, uint32_t tag,
-                                                uint32_t* err, RouteLds& L) {
-  if (!p.ids_in) route_need(p, lane, rwc, 1u << (kRwId + j), tag, err, L);
-  const uint32_t w = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwId + j);
-  return (w != kUnseenWord && (int)w < p.E) ? (int)w : -1;
-}
 
 // SwiGLU of gate/up row pairs [i0, i0 + kPairs): kPairs / 2 tagged activation pairs.
 template <int MH, bool EXACT, typename Take>
@@ -511,15 +464,17 @@ __device__ __forceinline__ void top8_bitonic(const float (&v)[4], int E, int k, 
   }
 }
 
-// The K task: gather every tagged logit, select the top-k, publish the routing.
-// Kept compact (rolled rounds, per-slot values held by lane r): this runs once
-// per call on a cold instruction cache while the rest of the GPU streams, so code
-// size is latency here.
-template <int MAXEPL, typename Take>
-__device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane, uint32_t tag, uint32_t* err,
-                                                Take&& take) {
+// A block's routing: one wave of the block gathers every tagged logit of the block's copy,
+// selects the top-k, computes the softmax weights and the shared gate, and writes the
+// route words to LDS for the whole block.  Every block resolves the routing itself: the
+// selection is one wave's instruction latency (1.3-1.6 us), and no further hand-off
+// through memory follows it.
+template <int MAXEPL>
+__device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, uint32_t tag, uint32_t* err,
+                                              RouteLds& L) {
   const bool has_sh = p.sh_gate != nullptr;
   __builtin_amdgcn_s_setprio(3);   // the routing gates every expert task: issue ahead of streaming waves
+  const uint64_t* lg = p.lg64 + (size_t)(blockIdx.x % kLogitReplicas) * p.lg_stride;
   float v[MAXEPL];
   float gl = 0.f;
   if (p.logits_in) {
@@ -536,8 +491,8 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
     for (;;) {
       uint64_t w[MAXEPL];
 #pragma unroll
-      for (int i = 0; i < MAXEPL; ++i) w[i] = ld64c(p.lg64 + min(lane + 64 * i, p.E - 1));
-      const uint64_t wg = ld64c(p.lg64 + p.E);
+      for (int i = 0; i < MAXEPL; ++i) w[i] = ld64c(lg + min(lane + 64 * i, p.E - 1));
+      const uint64_t wg = ld64c(lg + p.E);
       bool ok = !has_sh || has_tag(wg, tag);
       gl = __uint_as_float((uint32_t)wg);
       if (!p.logits_in) {
@@ -552,7 +507,6 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
       if (!b.step(err)) break;
     }
   }
-  take();
   int my_id = p.E;          // lane r < k: slot r's expert and logit
   float my_lw = -INFINITY;
   float m = 0.f;            // the largest logit (slot 0)
@@ -604,14 +558,6 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
       if (r == 0) m = g;
     }
   }
-  // Publish the ids at once (the gate/up tasks need nothing else): lane l writes
-  // id word l % 8 of replica l / 8 (one store instruction per 8 replicas).
-#pragma unroll
-  for (int it = 0; it < kRouteReplicas / 8; ++it) {
-    const int slot = lane & 7;
-    const uint32_t id = (uint32_t)__builtin_amdgcn_ds_bpermute(slot * 4, my_id);
-    if (slot < p.k) st64c(route_line(p, it * 8 + (lane >> 3)) + kRwId + slot, tagged(tag, id));
-  }
   // Softmax over all E in fp32 (max-subtracted), renormalised over the k
   // selected, rounded to bf16 -- one slot per lane.
   float ls = 0.f;
@@ -624,29 +570,59 @@ __device__ __forceinline__ void resolve_routing(const DecodeParams& p, int lane,
   const float psum = wave_sum(pr);   // all lanes active: a DPP reduction must not run divergent
   const float wr = (mine && my_id < p.E) ? rbf16(pr / psum) : 0.f;
   const uint32_t wb = f32_to_bf16(wr);
-  // Then the weights and the gate: lane l < 8 holds weight l, lane 8 the gate;
-  // word w (0..8) of replica r is written by flattened lane r * 9 + w.
-  uint32_t word = wb;
-  if (lane == 8) word = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
-#pragma unroll
-  for (int it = 0; it < (kRouteReplicas * 9 + 63) / 64; ++it) {
-    const int f = it * 64 + lane;
-    const int w9 = f % 9;
-    const uint32_t val = (uint32_t)__builtin_amdgcn_ds_bpermute(w9 * 4, (int)word);
-    const bool used = w9 < p.k || (w9 == 8 && has_sh);
-    if (f < kRouteReplicas * 9 && used)
-      st64c(route_line(p, f / 9) + (w9 == 8 ? kRwGate : kRwW + w9), tagged(tag, val));
-  }
-  if (mine) {
-    if (p.ids_out) p.ids_out[lane] = my_id;
-    if (p.w_out) p.w_out[lane] = wb;
-    if (p.heat && my_id < p.E) atomicAdd(p.heat + my_id, 1u);
-  }
-  if (p.logits_out)
-#pragma unroll
-    for (int i = 0; i < MAXEPL; ++i)
-      if (lane + 64 * i < p.E) p.logits_out[lane + 64 * i] = v[i];
+  // Route words: lanes 0..7 the ids (E for slots past k), lanes 8..15 the weights of
+  // slots 0..7, lane 16 the gate.
+  const uint32_t wsrc = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane - kRwW) & 63) * 4, (int)wb);
+  const uint32_t gate = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
+  const uint32_t word = lane < kRwW ? (uint32_t)my_id : lane < kRwGate ? wsrc : gate;
+  if (lane < kRouteWords) L.word[lane] = word;
+  __threadfence_block();
+  if (lane == 0) __hip_atomic_store(&L.valid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   __builtin_amdgcn_s_setprio(0);
+}
+
+// The wave's routing cache `rwc` (lane l < kRouteWords holds route word l) from the
+// block's copy in LDS, resolved first by whichever wave of the block gets there first.
+__device__ __forceinline__ void route_fetch(const DecodeParams& p, int lane, uint32_t& rwc, uint32_t tag,
+                                           uint32_t* err, RouteLds& L) {
+  Backoff<16> b;
+  for (;;) {
+    if (__hip_atomic_load(&L.valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) break;
+    uint32_t got = 0;
+    if (lane == 0) got = atomicCAS(&L.poller, 0u, 1u) == 0u;
+    if (__builtin_amdgcn_readfirstlane(got)) {
+      if (p.E <= 256)
+        resolve_block<4>(p, lane, tag, err, L);
+      else
+        resolve_block<16>(p, lane, tag, err, L);
+      break;
+    }
+    if (!b.step(err)) break;
+  }
+  __threadfence_block();
+  if (lane < kRouteWords) rwc = L.word[lane];
+}
+
+// The call's routing outputs (ids, bf16 weights, heat counts, logits), written once: by
+// the wave that runs the first gate/up task.
+__device__ __forceinline__ void publish_routing(const DecodeParams& p, int lane, uint32_t rwc) {
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_ds_bpermute(((kRwW + lane) & 63) * 4, (int)rwc);
+  if (lane < p.k) {
+    if (p.ids_out) p.ids_out[lane] = (int64_t)rwc;
+    if (p.w_out) p.w_out[lane] = (uint16_t)wv;
+    if (p.heat && rwc < (uint32_t)p.E) atomicAdd(p.heat + rwc, 1u);
+  }
+  if (p.logits_out) {
+    const uint64_t* lg = p.lg64 + (size_t)(blockIdx.x % kLogitReplicas) * p.lg_stride;
+    for (int e = lane; e < p.E; e += 64)
+      p.logits_out[e] = p.logits_in ? p.logits_in[e] : __uint_as_float((uint32_t)ld64c(lg + e));
+  }
+}
+
+// Expert of slot j (wave-uniform) for this wave, or -1 for a skipped or invalid id.
+__device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, uint32_t rwc) {
+  const uint32_t w = (uint32_t)__builtin_amdgcn_readlane((int)rwc, kRwId + j);
+  return (w != kUnseenWord && (int)w < p.E) ? (int)w : -1;
 }
 
 // Router rows [4t, 4t + 4) of E + 1 (row E: the shared-gate weight).
@@ -667,12 +643,21 @@ __device__ __forceinline__ void task_router(const DecodeParams& p, int t, int la
   float d[kRouterRows];
   wave_dots_p<MH, kRouterRows, EXACT>(rp, xf, p.H, lane, d);
   take();
-  if (lane < kRouterRows && r0 + lane < n_rows) {
-    float v = d[0];
-#pragma unroll
-    for (int r = 1; r < kRouterRows; ++r) v = lane == r ? d[r] : v;
-    const int row = r0 + lane;
-    st64c(p.lg64 + (row < n_lrows ? row : p.E), tagged(tag, __float_as_uint(v)));
+  // One store instruction: lane l writes rows 2 (l % 2) and 2 (l % 2) + 1 of copy l / 2 as
+  // one 16-byte store of two tagged words (the task's rows are consecutive logit indices,
+  // E - 1 and E included; the shared-gate row alone, with logits supplied, is one word).
+  static_assert(kRouterRows == 4 && kLogitReplicas == 32, "4 rows x 32 copies in one store instruction");
+  const int ra = r0 + 2 * (lane & 1), rb = ra + 1;
+  const size_t ia = ra < n_lrows ? (size_t)ra : (size_t)p.E;
+  const uint32_t va = __float_as_uint((lane & 1) ? d[2] : d[0]);
+  const uint32_t vb = __float_as_uint((lane & 1) ? d[3] : d[1]);
+  uint64_t* dst = p.lg64 + (size_t)(lane >> 1) * p.lg_stride + ia;
+  if (rb < n_rows && ia + 1 == (rb < n_lrows ? (size_t)rb : (size_t)p.E)) {
+    st128c(dst, tagged(tag, va), tagged(tag, vb));
+  } else if (ra < n_rows) {
+    st64c(dst, tagged(tag, va));
+    if (rb < n_rows) st64c(p.lg64 + (size_t)(lane >> 1) * p.lg_stride + (rb < n_lrows ? (size_t)rb : (size_t)p.E),
+                           tagged(tag, vb));
   }
 }
 
@@ -687,10 +672,6 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
                                              uint32_t* err, RouteLds& L) {
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
-  if (!p.ids_in) {
-    const uint32_t slots = (1u << k) - 1u;
-    route_need(p, lane, rwc, (slots << kRwId) | (slots << kRwW) | (has_sh ? 1u << kRwGate : 0u), tag, err, L);
-  }
   const int r = lane & (kDownRows - 1);
   // Word j holds this lane's row of slot j (j < k - 1) or, at j = k - 1, of the
   // shared expert (slot k); words past that are never used.
@@ -752,10 +733,6 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
                                            RouteLds& L) {
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
-  if (!p.ids_in) {
-    const uint32_t slots = (1u << k) - 1u;
-    route_need(p, lane, rwc, (slots << kRwId) | (slots << kRwW) | (has_sh ? 1u << kRwGate : 0u), tag, err, L);
-  }
   const int r = lane & (RQ - 1);
   uint32_t pr[kFusedMaxK];   // word j: this lane's row of slot j (j < k - 1) or of the shared expert (j = k - 1)
   Backoff<4> b;
@@ -807,7 +784,7 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
 template <int MI, int RQ, typename Take>
 __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, int idx, int lane, uint32_t& rwc,
                                              uint32_t tag, uint32_t* err, RouteLds& L, Take&& take) {
-  const int e = wave_slot_expert(p, slot, lane, rwc, tag, err, L);
+  const int e = wave_slot_expert(p, slot, rwc);
   const int h0 = idx * RQ;
   float d[RQ];
 #pragma unroll
@@ -832,17 +809,13 @@ struct TaskRef {
   int type, slot, idx;
 };
 
-// Task t of the list R, K, then per slot j: Gj, D(j - kDownLag) once j >= kDownLag,
+// Task t of the list R, then per slot j: Gj, D(j - kDownLag) once j >= kDownLag,
 // S after G(sh_after) and SD after G(sd_after); then the remaining D.  Pure arithmetic on values
 // held in scalar registers: a lookup table in kernel-argument memory costs a
 // memory round trip per step.
 __device__ __forceinline__ TaskRef decode_task(const DecodeParams& p, int t) {
   if (t < p.n_r) return {kTR, 0, t};
   t -= p.n_r;
-  if (p.n_r) {
-    if (t == 0) return {kTK, 0, 0};
-    t -= 1;
-  }
   for (int j = 0; j < p.k; ++j) {
     if (t < p.n_g) return {kTG, j, t};
     t -= p.n_g;
@@ -870,7 +843,6 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
   if (wrap) {
     uint64_t* w = reinterpret_cast<uint64_t*>(p.handoff);
     for (size_t i = lane; i < p.handoff_words; i += 64) st64c(w + i, 0ull);
-    for (int i = lane; i < kRouteReplicas * kRouteStride * kLine; i += 64) st32c(line(p, kLnRoute) + i, 0u);
   }
   const uint32_t epoch = wrap ? 0u : tag;
   if (lane < kQueues) st32c(line(p, kLnQueue + lane) + kQueueEpochWord, epoch);
@@ -902,6 +874,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   }
   __syncthreads();
   uint32_t rwc = kUnseenWord;   // this wave's routing cache (lane layout of RouteWord)
+  bool routed = p.ids_in != nullptr;
   if (p.ids_in) {
     // Caller-supplied routing (ids outside [0, E) are skipped; E is the sentinel).
     if (lane0 < p.k) {
@@ -944,17 +917,19 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
     const TaskRef tk = decode_task(p, t);
+    if (!routed && (tk.type == kTG || tk.type == kTD)) {
+      // The first routed task of this wave: the block's routing, resolved by this
+      // wave or another of the block (one call site: the resolution is long code).
+      route_fetch(p, lane, rwc, tag, err, s_rt);
+      routed = true;
+      if (t == p.n_r) publish_routing(p, lane, rwc);   // task n_r: the first gate/up task of slot 0
+    }
     if (tk.type == kTR) {
       task_router<MH, EXACT>(p, tk.idx, lane, tag, take);
-    } else if (tk.type == kTK) {
-      if (p.E <= 256)
-        resolve_routing<4>(p, lane, tag, err, take);
-      else
-        resolve_routing<16>(p, lane, tag, err, take);
     } else if (tk.type == kTS || tk.type == kTG) {
       // Gate/up pairs: the shared expert (S) or routed slot j (G); one call site.
       const bool shared = tk.type == kTS;
-      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
+      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, rwc);
       const int n_rows = shared ? p.Is : p.I;
       if (Q4 && !shared) {
         if (e >= 0)
@@ -973,7 +948,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     } else {
       // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
-      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, lane, rwc, tag, err, s_rt);
+      const int e = shared ? 0 : wave_slot_expert(p, tk.slot, rwc);
       const int h0 = tk.idx * kDownRows;
       float d[kDownRows] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (e >= 0) {
@@ -1116,7 +1091,7 @@ int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   // behind a full memory queue waits microseconds, and every routing step is one.
   p.sh_after = p.k - 1 < kSharedAfter ? p.k - 1 : kSharedAfter;
   p.sd_after = p.k - 1 < p.sh_after + kDownLag ? p.k - 1 : p.sh_after + kDownLag;
-  p.n_tasks = p.n_r + (p.n_r ? 1 : 0) + p.n_s + p.n_sd + p.k * (p.n_g + p.n_d);
+  p.n_tasks = p.n_r + p.n_s + p.n_sd + p.k * (p.n_g + p.n_d);
   int grid = resident_blocks(k);
   if (grid <= 0) return TMOE_ERR_HIP;
   const int need = (p.n_tasks + kWaves - 1) / kWaves;

@@ -35,7 +35,8 @@ struct DecodeParams {
   uint16_t* sh_ws;            // [H]
   // fused task graph (tmoe_decode_fused)
   uint32_t* sync;             // task-graph lines
-  uint64_t* lg64;             // [E + 1] tagged fp32 logits (index E: shared-gate logit)
+  uint64_t* lg64;             // [kLogitReplicas][lg_stride] tagged fp32 logits (index E: shared-gate logit)
+  int lg_stride;              // u64 words per logit copy
   uint64_t* act64;            // [k * I / 2] tagged bf16 activation pairs, then [Is / 2] shared
   uint64_t* dq64;             // [(k + 1) * H] tagged per-slot down results (slot k: shared, before its gate):
                               // bf16 row pairs, or one fp32 row per word in int4 mode

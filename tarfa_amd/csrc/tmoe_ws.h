@@ -22,25 +22,26 @@ enum ErrorBit { kErrExpertId = 1u, kErrTimeout = 2u };
 // tag}: the tag is the call's epoch, so words left by earlier calls never match
 // and nothing is cleared between calls.
 constexpr int kLine = 64;                 // uint32 per line
-constexpr int kRouteReplicas = 32;        // routing published to this many lines ...
-constexpr int kRouteStride = 16;          // ... 16 lines (4 KB) apart, on different memory channels
+constexpr int kLogitReplicas = 32;        // router logits published to this many copies (blocks poll one each)
 constexpr int kQueues = 32;               // task queues: 4 waves x 8 XCD-sized groups of blocks
 enum SyncLine {
   kLnEpoch = 0,                           // word 0: epoch of the next call (tag = epoch + 1)
   kLnQueuesDone = 1,                      // queues fully drained this call
   kLnQueue = 2,                           // [kQueues] word kQueueEpochWord: epoch copy for the queue's waves
   kLnQueueExit = kLnQueue + kQueues,      // [kQueues] waves that left each queue
-  kLnRoute = kLnQueueExit + kQueues,      // [kRouteReplicas * kRouteStride] replica r at line r * kRouteStride
-  kSyncLines = kLnRoute + kRouteReplicas * kRouteStride,
+  kSyncLines = kLnQueueExit + kQueues,
 };
 // Each queue line also carries a copy of the epoch, read by that queue's waves
 // (coherent loads of one line serialise, so 2048 waves must not share one word).
 constexpr int kQueueEpochWord = 16;
 // Each queue's exit line also holds its ticket counter (drawn once per task).
 constexpr int kQueueDrawWord = 32;
-// u64 words {payload, tag} of a route replica line: the expert ids of slots 0..7,
-// their bf16 weights, the shared-expert bf16 gate.  Ids are published first.
+// Words of a block's routing (LDS, lane layout of a wave's routing cache): the expert ids
+// of slots 0..7, their bf16 weights, the shared-expert bf16 gate.
 enum RouteWord { kRwId = 0, kRwW = 8, kRwGate = 16, kRouteWords = 17 };
+// u64 words per logit copy: E + 1 (index E: the shared-gate logit), rounded up to whole
+// 256-byte lines.
+inline int logit_stride(int E) { return ((E + 1) + 31) & ~31; }
 
 struct Ws {
   size_t status;   // uint32[kStatusSlots]
@@ -56,8 +57,8 @@ struct Ws {
   size_t inv;      // int32[T * k]
   size_t scratch;  // int32[E + 64]      dispatch counters
   size_t ch;       // bf16[T * k * H]    weighted per-assignment expert outputs (T > 1)
-  size_t tagged;   // u64[(E + 1) + (k * I + Is) / 2 + (k + 1) * H]  tagged logits, activation
-                   // pairs, per-slot down results (slot k = shared expert)
+  size_t tagged;   // u64[kLogitReplicas * logit_stride(E) + (k * I + Is) / 2 + (k + 1) * H]  tagged
+                   // logit copies, activation pairs, per-slot down results (slot k = shared expert)
   size_t total;
 };
 
@@ -82,7 +83,8 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.inv = take(sizeof(int32_t) * t * (size_t)k);
   w.scratch = take(sizeof(int32_t) * (size_t)(E + 64));
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
-  w.tagged = take(8 * ((size_t)(E + 1) + ((size_t)k * I + (size_t)Is) / 2 + (size_t)(k + 1) * H));
+  w.tagged = take(8 * ((size_t)kLogitReplicas * logit_stride(E) + ((size_t)k * I + (size_t)Is) / 2 +
+                        (size_t)(k + 1) * H));
   w.total = o;
   return w;
 }
