@@ -68,6 +68,9 @@ namespace tmoe {
 constexpr int kWaves = 4;              // waves per block
 constexpr int kRouterRows = 4;         // router rows per R task
 constexpr int kPairs = 2;              // gate/up row pairs per G / S task (4 rows of K = H in flight)
+constexpr int kQ4SPairs = 4;           // int4 mode: row pairs per (bf16) S task -- 8 rows in flight: the
+                                       // int4 tasks leave registers for them, and half as many S tasks
+                                       // finish the shared expert sooner in the routing window
 constexpr int kDownRows = 8;           // down rows per D / SD task (8 rows of K = I in flight)
 constexpr int kQ4Pairs = 4;            // int4: gate/up row pairs per G task (8 rows of H/2 bytes)
 // int4: down rows per D task (their scale words, rows * I / 256, fit two per lane)
@@ -199,34 +202,34 @@ struct RouteLds {
 };
 constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
 
-// SwiGLU of gate/up row pairs [i0, i0 + kPairs): kPairs / 2 tagged activation pairs.
-template <int MH, bool EXACT, typename Take>
+// SwiGLU of gate/up row pairs [i0, i0 + P): P / 2 tagged activation pairs.
+template <int MH, bool EXACT, int P, typename Take>
 __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* up, int i0, int n_rows, int K,
                                          const uint16_t* x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
-  static_assert(kPairs % 2 == 0, "activations are published as tagged bf16 pairs");
+  static_assert(P % 2 == 0, "activations are published as tagged bf16 pairs");
   XPack<MH> xf;
   load_xpack<MH, EXACT>(xf, x, K, lane);
-  const uint16_t* rows[2 * kPairs];
+  const uint16_t* rows[2 * P];
 #pragma unroll
-  for (int q = 0; q < kPairs; ++q) {
+  for (int q = 0; q < P; ++q) {
     const int i = min(i0 + q, n_rows - 1);
     rows[q] = gate + (size_t)i * K;
-    rows[kPairs + q] = up + (size_t)i * K;
+    rows[P + q] = up + (size_t)i * K;
   }
-  float d[2 * kPairs];
-  wave_dots_p<MH, 2 * kPairs, EXACT>(rows, xf, K, lane, d);
-  int pk[kPairs / 2];
+  float d[2 * P];
+  wave_dots_p<MH, 2 * P, EXACT>(rows, xf, K, lane, d);
+  int pk[P / 2];
 #pragma unroll
-  for (int h = 0; h < kPairs / 2; ++h) {
+  for (int h = 0; h < P / 2; ++h) {
     const int i = i0 + 2 * h;
-    const uint32_t a0 = i < n_rows ? f32_to_bf16(swiglu_bf16(rbf16(d[2 * h]), rbf16(d[kPairs + 2 * h]))) : 0u;
+    const uint32_t a0 = i < n_rows ? f32_to_bf16(swiglu_bf16(rbf16(d[2 * h]), rbf16(d[P + 2 * h]))) : 0u;
     const uint32_t a1 =
-        i + 1 < n_rows ? f32_to_bf16(swiglu_bf16(rbf16(d[2 * h + 1]), rbf16(d[kPairs + 2 * h + 1]))) : 0u;
+        i + 1 < n_rows ? f32_to_bf16(swiglu_bf16(rbf16(d[2 * h + 1]), rbf16(d[P + 2 * h + 1]))) : 0u;
     pk[h] = (int)(a0 | (a1 << 16));
   }
   const uint32_t word = (uint32_t)spread(pk);
   take();
-  if (lane < kPairs / 2 && i0 + 2 * lane < n_rows) st64c(act64 + i0 / 2 + lane, tagged(tag, word));
+  if (lane < P / 2 && i0 + 2 * lane < n_rows) st64c(act64 + i0 / 2 + lane, tagged(tag, word));
 }
 
 // 8 rows of one down projection: d[r] = bf16(dot(w[h0 + r], act)).  The weight
@@ -940,7 +943,8 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
         const uint16_t* g = shared ? p.sh_gate : gu;
         const uint16_t* u = shared ? p.sh_up : gu + (size_t)p.I * p.H;
-        up_pairs<MH, EXACT>(g, u, tk.idx * kPairs, n_rows, p.H, p.x, lane,
+        constexpr int P = Q4 ? kQ4SPairs : kPairs;
+        up_pairs<MH, EXACT, P>(g, u, tk.idx * P, n_rows, p.H, p.x, lane,
                             p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag, take);
       }
     } else if (Q4 && tk.type == kTD) {
@@ -1078,7 +1082,8 @@ int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
     return TMOE_ERR_SHAPE;
   const int n_rows = (p.logits_in ? 0 : p.E) + (has_sh ? 1 : 0);
   p.n_r = run_router ? (n_rows > 0 ? (n_rows + kRouterRows - 1) / kRouterRows : 1) : 0;
-  p.n_s = has_sh ? (p.Is + kPairs - 1) / kPairs : 0;
+  const int s_pairs = p.q4 ? kQ4SPairs : kPairs;
+  p.n_s = has_sh ? (p.Is + s_pairs - 1) / s_pairs : 0;
   p.n_sd = has_sh ? p.H / kDownRows : 0;
   if (p.q4) {
     p.n_g = p.I / kQ4Pairs;
