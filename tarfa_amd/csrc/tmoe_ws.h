@@ -18,7 +18,7 @@ enum ErrorBit { kErrExpertId = 1u, kErrTimeout = 2u };
 // 256-byte line (64 uint32): atomics on one hot line serialise at ~11 ns each.
 // Counters are zero between calls (the last wave to leave a queue re-zeroes its
 // exit count).  Hand-off words
-// (logits, routing, activations, per-slot down results) are 64-bit {payload,
+// (logits, activations, per-slot down results) are 64-bit {payload,
 // tag}: the tag is the call's epoch, so words left by earlier calls never match
 // and nothing is cleared between calls.
 constexpr int kLine = 64;                 // uint32 per line
