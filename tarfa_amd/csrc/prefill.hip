@@ -11,6 +11,7 @@
 //             rounding after each add, then + sh          fused_int4.py:244 (index_add_),
 //                                                          transformers/.../modeling_qwen3_5_moe.py:796
 // The shared expert is one more group (id E) whose rows are all T tokens in order.
+#include <type_traits>
 #include "tmoe_gemv.h"
 #include "tmoe_ws.h"
 
@@ -57,10 +58,12 @@ int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, fl
 }
 
 // ---------------------------------------------------------------- dispatch
-// One block of 1024 threads: per-expert counts, offsets, M-chunk schedule, inv := -1.
+// One block of 1024 threads: per-expert counts, offsets, M-chunk schedule, inv := -1, and
+// (desc non-null) one descriptor per M-chunk: {group, rows, first row in group order, 0}.
 __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, const int64_t* ids64, int T, int k,
                                                          int E, int shared_rows, int32_t* offsets,
-                                                         int32_t* tile_start, int32_t* inv, uint32_t* status) {
+                                                         int32_t* tile_start, int32_t* inv, uint32_t* status,
+                                                         int4* desc) {
   __shared__ int cnt[1024];
   const int tid = threadIdx.x;
   for (int e = tid; e < 1024; e += 1024) cnt[e] = 0;
@@ -94,6 +97,22 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, c
   if (tid < E) offsets[tid + 1] = sc[tid];
   if (tid == 0) { offsets[0] = 0; tile_start[0] = 0; }
   if (tid <= E) tile_start[tid + 1] = sk[tid];
+  if (!desc) return;
+  // M-chunk mt of group g (sk[g - 1] <= mt < sk[g]): rows r0 = (mt - sk[g - 1]) kBM onwards.
+  const int n_groups = shared_rows > 0 ? E + 1 : E;
+  const int n_chunks = sk[n_groups - 1];
+  for (int mt = tid; mt < n_chunks; mt += 1024) {
+    int lo = 0, hi = n_groups - 1;              // the first g with sk[g] > mt
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sk[mid] > mt) hi = mid; else lo = mid + 1;
+    }
+    const int g = lo;
+    const int r0 = (mt - (g ? sk[g - 1] : 0)) * kBM;
+    const int rows = g < E ? cnt[g] : shared_rows;
+    const int first = g < E ? (g ? sc[g - 1] : 0) : 0;
+    desc[mt] = int4{g, min(kBM, rows - r0), first + r0, 0};
+  }
 }
 
 // One block per expert: stable compaction of the slot-major traversal j = slot*T + t.
@@ -148,11 +167,9 @@ struct GemmParams {
   const uint16_t* shw0;      // shared: gate_proj (up) / down_proj (down)
   const uint16_t* shw1;      // shared: up_proj (up)
   int shared_row0;           // first act row of the shared group (T * k)
-  uint16_t* out;             // up: act; down: ch [T*k, H]
-  uint16_t* out_sh;          // down: sh [T, H]
-  const float* wf;           // routing weights by assignment t*k + slot (fp32 holding bf16) ...
-  const uint16_t* wb;        // ... or bf16
-  const float* gs;           // [T] shared gate
+  uint16_t* out;             // up: act; down: ch [T*k, H], each expert output unscaled
+  uint16_t* out_sh;          // down: sh [T, H], the shared expert's output before its gate
+  const int4* desc;          // persistent kernel: M-chunk descriptors {group, rows, first row, 0}
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -388,84 +405,494 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
         const uint16_t v = f32_to_bf16(swiglu_bf16(rbf16(acc[sub][0][i]), rbf16(acc[sub][1][i])));
         if (row < m) o[(size_t)row * p.N] = v;
       }
-  } else if (shared) {
-    uint16_t* o = p.out_sh + (size_t)r0 * p.N + col;
-#pragma unroll
-    for (int sub = 0; sub < kSubs; ++sub)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = sub * 16 + rl + i;
-        const float gv = p.gs[r0 + min(row, m - 1)];
-        const uint16_t v0 = f32_to_bf16(gv * rbf16(acc[sub][0][i])), v1 = f32_to_bf16(gv * rbf16(acc[sub][1][i]));
-        if (row < m) { o[(size_t)row * p.N] = v0; o[(size_t)row * p.N + 16] = v1; }
-      }
   } else {
-    uint16_t* o = p.out + (size_t)(grow0 + r0) * p.N + col;
-    const int32_t* pr = p.perm + grow0 + r0;
+    // Down: the expert's (or the shared expert's) output, unscaled; the combine applies
+    // the routing weight (or the shared gate).
+    uint16_t* o = shared ? p.out_sh + (size_t)r0 * p.N + col : p.out + (size_t)(grow0 + r0) * p.N + col;
 #pragma unroll
     for (int sub = 0; sub < kSubs; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = sub * 16 + rl + i;
-        const int a = pr[min(row, m - 1)];
-        const float w = p.wf ? p.wf[a] : bf16_to_f32(p.wb[a]);
-        const uint16_t v0 = f32_to_bf16(rbf16(acc[sub][0][i]) * w), v1 = f32_to_bf16(rbf16(acc[sub][1][i]) * w);
+        const uint16_t v0 = f32_to_bf16(acc[sub][0][i]), v1 = f32_to_bf16(acc[sub][1][i]);
         if (row < m) { o[(size_t)row * p.N] = v0; o[(size_t)row * p.N + 16] = v1; }
       }
   }
 }
 
+// ---------------------------------------------------------------- grouped GEMM, persistent
+// One block of 8 waves per CU, walking a list of tiles with one continuous load pipeline:
+// the loads of a tile's first stages are issued during the previous tile's last stages, so
+// no tile pays a pipeline fill.  Tile: kBM rows of one group x 8 waves x 32 weight rows
+// (up: 16 gate rows and the matching 16 up rows per wave, 128 activation columns per
+// tile; down: 32 output columns per wave, 256 per tile), K in stages of 64.
+//   A (the group's rows, contiguous: the gathered token rows for up, the activations for
+//   down) goes global -> LDS directly (global_load_lds_dwordx4, lane l's 16 bytes land at
+//   16 l of the load's 1 KB): a load covers 8 whole rows of the stage (8 x 128 B, full
+//   cache lines), lane l taking row l / 8 and 16-byte chunk (l % 8) ^ (l / 8).  Row r's
+//   chunk c thus sits in LDS chunk c ^ (r % 8): the MFMA's 16-byte fragment reads (16
+//   rows, one chunk) hit 8 distinct chunks per 8 lanes, conflict-free.  20 loads per
+//   stage over 8 waves: each wave issues 3, the last 4 repeating loads 16..19 (the same
+//   bytes to the same place), so every wave issues the same sequence.
+//   B (the weights, each byte read once) goes straight into MFMA B-fragment registers
+//   with plain loads, kPB stages ahead.
+// Vector memory completes in issue order: the wait for weight stage s (issued kPB stages
+// ahead) also covers every older load, so about kPB stages of loads (~200 KB per CU) stay
+// in flight; the A ring is deeper (kPA stages) so that its waits never come first.
+// Tile data (group, rows, weight pointers) is read with scalar loads from the M-chunk
+// descriptors written by the dispatch.
+constexpr int kPW = 8;                  // waves per block
+constexpr int kPNB = 2;                 // 16-row weight blocks per wave
+constexpr int kPMB = kBM / 16;          // 16-row token blocks per tile
+constexpr int kPR = 8;                  // A ring slots in LDS (and the unrolled cycle)
+constexpr int kPA = kPR - 1;            // A stages loaded ahead
+constexpr int kPB = 4;                  // B ring slots in registers: B stages loaded ahead
+constexpr int kPSlot = kBM * 8;         // u32x4 per A slot (kBM rows x 128 B = 20 KB)
+constexpr int kPLoads = 3;              // A loads per wave per stage
+constexpr int kPUpCols = 16 * kPW, kPDnCols = 32 * kPW;
+static_assert(kBM / 8 <= kPW * kPLoads && kBM / 8 > kPW * (kPLoads - 1), "A loads cover the stage once");
+
+// s_waitcnt vmcnt(N), as inline asm: the compiler does not see the pipeline's loads, so a
+// builtin wait could look redundant to it and be dropped.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+// Scalar loads of launch-constant data (written by an earlier kernel), waited for at once.
+// The address is wave-uniform; readfirstlane puts it in SGPRs for the compiler too.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int sload1(const void* p) {
+  p = uniform_ptr(p);
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ i32x4 sload4(const void* p) {
+  p = uniform_ptr(p);
+  i32x4 v;
+  asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ const void* sload_ptr(const void* p) {
+  p = uniform_ptr(p);
+  i32x2 v;
+  asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return reinterpret_cast<const void*>(((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x);
+}
+
+// Pipeline loads as inline asm: the compiler does not count them, so its own waits (for
+// the loads it does see) can only come out stricter, and it inserts none for these; the
+// kernel waits for them explicitly.  Uniform base (SGPRs) + 32-bit per-lane byte offset.
+__device__ __forceinline__ u32x4 gld16(const void* sbase, uint32_t voff) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
+  return v;
+}
+__device__ __forceinline__ uint32_t gld4(const void* sbase, uint32_t voff) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
+  return v;
+}
+// 16 bytes per lane from global memory straight into LDS at lds + 16 lane (M0 = lds).
+// Nothing else in the kernel uses M0.
+__device__ __forceinline__ void gdma16(const void* sbase, uint32_t voff, const void* lds) {
+  const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(l) : "memory");
+}
+
+// One wave's view of one tile (all wave-uniform).
+struct PTile {
+  int arow0;                // A row of the tile's first row (gather: its position in perm)
+  bool gather;              // up, routed: A rows are x[perm[arow0 + r] / k]
+  const uint16_t* b[kPNB];  // bf16: this wave's weight rows (row + lane's row and k offset added later)
+  const uint8_t* q[kPNB];   // int4: packed rows
+  const uint16_t* sc[kPNB]; // int4: scale rows
+  uint16_t* o;              // first output row, this tile's first column
+  int m;                    // valid rows
+};
+
+template <bool Q4>
+__global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
+  __shared__ u32x4 lA0[kPSlot], lA1[kPSlot], lA2[kPSlot], lA3[kPSlot], lA4[kPSlot], lA5[kPSlot], lA6[kPSlot],
+      lA7[kPSlot];
+  u32x4* const slots[kPR] = {lA0, lA1, lA2, lA3, lA4, lA5, lA6, lA7};
+  static_assert(kPR == 8, "one LDS array per ring slot");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = p.K;
+  const int cols = p.up ? kPUpCols : kPDnCols;
+
+  // Tiles f = (M-chunk - c_lo) * n_ntiles + N-tile.  XCD x (blocks b with b % 8 == x) takes
+  // the contiguous range [x per_xcd, (x + 1) per_xcd); its blocks interleave over it, so the
+  // N-tiles of one group run together on one XCD and share its L2 copy of the group's rows.
+  const int c_lo = sload1(p.tile_start + p.group_lo);
+  const int c_hi = sload1(p.tile_start + p.group_hi);
+  const int total = (c_hi - c_lo) * p.n_ntiles;
+  const int nbx = (int)gridDim.x >> 3;              // blocks per XCD
+  const int xcd = (int)blockIdx.x & 7, qb = (int)blockIdx.x >> 3;
+  const int per_xcd = (total + 7) / 8;
+  const int f0 = xcd * per_xcd + qb;
+  const int f_end = min(total, (xcd + 1) * per_xcd);
+  if (f0 >= f_end) return;
+  const int ntile = (f_end - f0 + nbx - 1) / nbx;
+
+  auto tile = [&](int j) {
+    const int f = f0 + j * nbx;
+    const int mt = c_lo + f / p.n_ntiles, nt = f % p.n_ntiles;
+    const i32x4 d = sload4(p.desc + mt);
+    const int g = d.x, row0 = d.z;
+    const bool shared = g == p.E;
+    PTile t;
+    t.m = d.y;
+    t.gather = p.up && !shared;
+    t.arow0 = (!p.up && shared ? p.shared_row0 : 0) + row0;
+    const int c0 = p.up ? nt * kPUpCols + wid * 16 : nt * kPDnCols + wid * 32;
+    if (p.up) t.o = p.out + (size_t)(shared ? p.shared_row0 + row0 : row0) * p.N + nt * kPUpCols;
+    else t.o = (shared ? p.out_sh : p.out) + (size_t)row0 * p.N + nt * kPDnCols;
+    if constexpr (Q4) {
+      const int part = p.up ? 0 : 2;
+      const uint8_t* pk = reinterpret_cast<const uint8_t*>(sload_ptr(p.table + 4 * g + part));
+      const uint16_t* sc = reinterpret_cast<const uint16_t*>(sload_ptr(p.table + 4 * g + part + 1));
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb) {
+        const int wr = p.up ? (nb ? p.I : 0) + c0 : c0 + 16 * nb;
+        t.q[nb] = pk + (size_t)wr * (K / 2);
+        t.sc[nb] = sc + (size_t)wr * (K / 128);
+        t.b[nb] = nullptr;
+      }
+    } else {
+      const uint16_t *w0, *w1;
+      if (shared) {
+        w0 = p.shw0;
+        w1 = p.up ? p.shw1 : p.shw0;
+      } else {
+        w0 = w1 = reinterpret_cast<const uint16_t*>(sload_ptr(p.table + 2 * g + (p.up ? 0 : 1)));
+      }
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb) {
+        const int wr = p.up ? ((nb && !shared) ? p.I : 0) + c0 : c0 + 16 * nb;
+        t.b[nb] = (nb ? w1 : w0) + (size_t)wr * K;
+        t.q[nb] = nullptr;
+        t.sc[nb] = nullptr;
+      }
+    }
+    return t;
+  };
+
+  PTile cur, nxt;   // the tile being multiplied and the one after it
+
+  // Lane constants.  A: load j of this wave covers rows 8 x .. 8 x + 7 (x = wid + 8 j, the
+  // last four repeating 16..19); B: row lane % 16 of each block, k offset 8 (lane / 16).
+  const int lrow = lane & 15, lk = 8 * (lane >> 4);
+  int a_row[kPLoads];
+#pragma unroll
+  for (int j = 0; j < kPLoads; ++j) {
+    const int x = wid + kPW * j;
+    a_row[j] = 8 * (x < kBM / 8 ? x : x - kPW / 2) + (lane >> 3);
+  }
+  const int a_col = 8 * ((lane & 7) ^ (lane >> 3));
+  const int a_rd0 = lrow * 8 + ((lane >> 4) ^ (lrow & 7));
+  const int a_rd1 = lrow * 8 + ((4 + (lane >> 4)) ^ (lrow & 7));
+
+  f32x4 acc[kPMB][kPNB];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < kPMB; ++i)
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb) acc[i][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  u32x4 breg[kPB][kPNB][2];
+  uint32_t qreg[kPB][kPNB][2], sreg[kPB][kPNB];
+  const int nk = K / kBK;   // a multiple of kPR
+  // Stage st of tile cur, or (nx) stage st of tile nxt: the pointers are selected, not
+  // branched on, so every path issues the same loads.
+  // Addresses: a wave-uniform base (SGPRs) plus a 32-bit per-lane byte offset, the
+  // global_load saddr form.  A offsets depend on the tile's row count (rows past it repeat
+  // the last row) and are kept for the current and the next tile.
+  const uint32_t b_off = (uint32_t)((lrow * K + lk) * 2);
+  const uint32_t q_off = (uint32_t)(lrow * (K / 2) + lk / 2);
+  const uint32_t s_off = (uint32_t)(lrow * (K / 128) * 2);
+  // A rows: up: x[perm[arow0 + r] / k] (routed) or x[arow0 + r] (shared); down:
+  // act[arow0 + r].  Rows past the tile's count repeat its last row.  The perm entries of
+  // a tile are fetched (pipeline loads, not counted by the compiler) a whole tile before
+  // its offsets are formed; by then the stage waits have covered them.
+  uint32_t a_off_cur[kPLoads], a_off_nxt[kPLoads];
+  uint32_t pv_cur[kPLoads], pv_nxt[kPLoads];
+  auto fetch_perm = [&](uint32_t* pv, const PTile& t) {
+    if (!t.gather) return;
+    const int32_t* pp = p.perm + t.arow0;
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) pv[j] = gld4(pp, (uint32_t)(min(a_row[j], t.m - 1) * 4));
+  };
+  auto a_offsets = [&](uint32_t* o, uint32_t* pv, const PTile& t) {
+    asm volatile("" : "+v"(pv[0]), "+v"(pv[1]), "+v"(pv[2]));
+    static_assert(kPLoads == 3, "three perm words per lane");
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) {
+      const int row = t.gather ? (int)pv[j] / p.k : t.arow0 + min(a_row[j], t.m - 1);
+      o[j] = (uint32_t)row * (uint32_t)(K * 2) + (uint32_t)(a_col * 2);
+    }
+  };
+  auto gaddr = [](const void* base, size_t ofs) {
+    return reinterpret_cast<const char*>(base) + ofs;
+  };
+  auto dma_a = [&](int slot, bool nx, int st) {
+    const char* ta = gaddr(p.a, (size_t)st * kBK * 2);
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) {
+      const int x = wid + kPW * j;
+      gdma16(ta, nx ? a_off_nxt[j] : a_off_cur[j], slots[slot] + (x < kBM / 8 ? x : x - kPW / 2) * 64);
+    }
+  };
+  auto load_b = [&](int slot, bool nx, int st) {
+    const int k0 = st * kBK;
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) {
+      if constexpr (Q4) {
+        const char* qr = gaddr(nx ? nxt.q[nb] : cur.q[nb], (size_t)k0 / 2);
+        qreg[slot][nb][0] = gld4(qr, q_off);
+        qreg[slot][nb][1] = gld4(qr + 16, q_off);
+        // The 32-bit word holding this stage's scale (table entries are 16-byte aligned
+        // and K / 128 is even here); multiply() takes its half.
+        sreg[slot][nb] = gld4(gaddr(nx ? nxt.sc[nb] : cur.sc[nb], (size_t)((k0 / 128) & ~1) * 2), s_off);
+      } else {
+        const char* br = gaddr(nx ? nxt.b[nb] : cur.b[nb], (size_t)k0 * 2);
+        breg[slot][nb][0] = gld16(br, b_off);
+        breg[slot][nb][1] = gld16(br + 64, b_off);
+      }
+    }
+  };
+  // Wait for B slot bs (issued kPB - 1 iterations and one A group before): at most the
+  // loads of the kPB - 1 later iterations and this iteration's A loads stay outstanding.
+  // The registers pass through the asm, so nothing reads them before the wait.
+  auto wait_b = [&](int bs) {
+    constexpr int n = (kPB - 1) * (kPLoads + 2 * kPNB + (Q4 ? kPNB : 0)) + kPLoads;
+    static_assert(n < 64, "vmcnt range");
+    if constexpr (Q4) {
+      asm volatile("s_waitcnt vmcnt(%4)"
+                   : "+v"(qreg[bs][0][0]), "+v"(qreg[bs][0][1]), "+v"(qreg[bs][1][0]), "+v"(qreg[bs][1][1])
+                   : "n"(n));
+      asm volatile("" : "+v"(sreg[bs][0]), "+v"(sreg[bs][1]));
+    } else {
+      asm volatile("s_waitcnt vmcnt(%4)"
+                   : "+v"(breg[bs][0][0]), "+v"(breg[bs][0][1]), "+v"(breg[bs][1][0]), "+v"(breg[bs][1][1])
+                   : "n"(n));
+    }
+  };
+  // Stage 8 c + u (A slot u, B slot u % kPB) takes scale 4 c + u / 2: the high half of its
+  // word for u = 2, 3, 6, 7.
+  auto multiply = [&](int u) {
+    const u32x4* la = slots[u];
+    const int bs = u % kPB;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8_t b[kPNB];
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb) {
+        if constexpr (Q4) {
+          const uint32_t sr = sreg[bs][nb];
+          const uint32_t bits = ((u >> 1) & 1) ? (sr & 0xFFFF0000u) : (sr << 16);
+          b[nb] = as_bf16x8(dequant_frag(qreg[bs][nb][ks], __uint_as_float(bits)));
+        } else {
+          b[nb] = as_bf16x8(breg[bs][nb][ks]);
+        }
+      }
+      const u32x4* lh = la + (ks ? a_rd1 : a_rd0);
+#pragma unroll
+      for (int i = 0; i < kPMB; ++i) {
+        const bf16x8_t a = as_bf16x8(lh[i * 128]);
+#pragma unroll
+        for (int nb = 0; nb < kPNB; ++nb)
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[i][nb], 0, 0, 0);
+      }
+    }
+  };
+  // Each stage ends with this wave's A loads of the next stage landed (everything but the
+  // last kPA - 1 stages' loads done: exact while only loads are outstanding, stricter right
+  // after an epilogue's stores) and a raw barrier: every wave's part of the next A stage is
+  // visible, and every wave is done reading the slot that the next stage refills.
+  // (__syncthreads' release fence would wait for every outstanding load, vmcnt(0), to
+  // cover the LDS writes of the direct loads.)
+  constexpr int kOpsPerStage = kPLoads + 2 * kPNB + (Q4 ? kPNB : 0);
+  static_assert((kPA - 1) * kOpsPerStage < 64, "vmcnt range");
+  auto barrier_raw = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto stage_end = [&]() {
+    wait_vmcnt<(kPA - 1) * kOpsPerStage>();
+    barrier_raw();
+  };
+
+  // Epilogue of a tile, staged through ring slot 7 (read by the tile's last stage; its
+  // next fill is issued after the epilogue) in passes of BPP 16-row blocks, so that every
+  // store is a whole 16-byte piece of an output row.  Row r's 16-byte chunk q sits at
+  // chunk q ^ 2 ((r / 4) % 4): the four row groups of one fragment write land in distinct
+  // banks.  C fragment: lane l holds rows 4 (l / 16) + e of each 16-row block, column
+  // l % 16; its rows' swizzle is 2 (l / 16).
+  auto epilogue = [&](const PTile& t, auto up_tag) {
+    constexpr bool UP = decltype(up_tag)::value;
+    constexpr int TCB = UP ? 2 * kPUpCols : 2 * kPDnCols;   // bytes per staged row
+    constexpr int BPP = UP ? 5 : 2;                         // 16-row blocks per pass
+    constexpr int RPP = 16 * BPP, CPR = TCB / 16;
+    static_assert(RPP * TCB <= kPSlot * 16 && kPMB % BPP == 0, "a pass fits in one ring slot");
+    char* stg = reinterpret_cast<char*>(slots[kPR - 1]);
+    const int sw = 2 * (lane >> 4), rl = 4 * (lane >> 4);
+    int cb[kPNB];
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) {
+      const int col = UP ? wid * 16 + lrow : wid * 32 + nb * 16 + lrow;
+      cb[nb] = rl * TCB + ((col >> 3) ^ sw) * 16 + (col & 7) * 2;
+    }
+#pragma unroll
+    for (int P = 0; P < kPMB / BPP; ++P) {
+#pragma unroll
+      for (int ii = 0; ii < BPP; ++ii) {
+        const int i = P * BPP + ii;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          char* rowp = stg + (ii * 16 + e) * TCB;
+          if constexpr (UP) {
+            *reinterpret_cast<uint16_t*>(rowp + cb[0]) =
+                f32_to_bf16(swiglu_bf16(rbf16(acc[i][0][e]), rbf16(acc[i][1][e])));
+          } else {
+#pragma unroll
+            for (int nb = 0; nb < kPNB; ++nb)
+              *reinterpret_cast<uint16_t*>(rowp + cb[nb]) = f32_to_bf16(acc[i][nb][e]);
+          }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      barrier_raw();
+      for (int x = tid; x < RPP * CPR; x += 64 * kPW) {
+        const int rr = x / CPR, qc = x - rr * CPR, row = P * RPP + rr;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * TCB + ((qc ^ (2 * ((rr >> 2) & 3))) * 16));
+        if (row < t.m) *reinterpret_cast<u32x4*>(t.o + (size_t)row * p.N + qc * 8) = v;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      barrier_raw();
+    }
+  };
+
+  cur = tile(0);
+  nxt = tile(min(1, ntile - 1));
+  fetch_perm(pv_cur, cur);
+  fetch_perm(pv_nxt, nxt);
+  wait_vmcnt<0>();
+  a_offsets(a_off_cur, pv_cur, cur);
+  a_offsets(a_off_nxt, pv_nxt, nxt);
+  // Prologue: the kPR iterations before stage 0, in the loop's own issue order (iteration
+  // v - kPR requests A stage v - 1 and B stage v - kPB), so the loads in flight at the top
+  // of the loop stand exactly as they do after every later cycle.
+#pragma unroll
+  for (int v = 0; v < kPR; ++v) {
+    if (v >= 1) dma_a(v - 1, false, v - 1);
+    if (v >= kPR - kPB) load_b(v - (kPR - kPB), false, v - (kPR - kPB));
+  }
+  stage_end();
+  // Stage st of tile j (A slot st % kPR, B slot st % kPB): refill the A slot read at the
+  // previous stage with stage st + kPA, multiply, refill this stage's B slot with stage
+  // st + kPB; stages past the tile's end are the next tile's first ones (for the last
+  // tile: its own first stages again, never multiplied).  K / 64 is a multiple of kPR, so
+  // tiles start on a cycle boundary and every load is unconditional.
+  auto cycle = [&](int st0, auto tail_tag) {
+    constexpr bool kTail = decltype(tail_tag)::value;   // the tile's last cycle
+#pragma unroll
+    for (int u = 0; u < kPR; ++u) {
+      const int sa = st0 + u + kPA, sb = st0 + u + kPB;
+      const bool na = kTail && u + kPA >= kPR, nb = kTail && u + kPB >= kPR;   // past the tile's end
+      dma_a((u + kPA) % kPR, na, na ? sa - nk : sa);
+      wait_b(u % kPB);
+      multiply(u);
+      load_b(u % kPB, nb, nb ? sb - nk : sb);
+      stage_end();
+    }
+  };
+  for (int j = 0; j < ntile; ++j) {
+    for (int st0 = 0; st0 < nk - kPR; st0 += kPR) cycle(st0, std::false_type{});
+    // The next tile's perm entries were fetched before this tile's first stage: the
+    // nk - kPR >= kPR stage waits since then leave only the last kPA - 1 stages' loads
+    // outstanding.
+    a_offsets(a_off_nxt, pv_nxt, nxt);
+    cycle(nk - kPR, std::true_type{});
+    if (p.up) epilogue(cur, std::true_type{});
+    else epilogue(cur, std::false_type{});
+    zero_acc();
+    cur = nxt;
+    nxt = tile(min(j + 2, ntile - 1));
+#pragma unroll
+    for (int q = 0; q < kPLoads; ++q) a_off_cur[q] = a_off_nxt[q];
+    fetch_perm(pv_nxt, nxt);
+  }
+  wait_vmcnt<0>();   // the last, unused stages landed before the block's LDS is released
+}
+
 // ---------------------------------------------------------------- combine
-// One wave per token; lane owns 8 columns per 512-column chunk.
+// One wave per token; lane owns 8 columns per 512-column chunk.  The GEMMs leave each
+// assignment's expert output and the shared expert's output unscaled (bf16 of the fp32
+// accumulator); this kernel applies the routing weight and the shared gate, each product
+// rounded to bf16, then accumulates in the reference's order (the token's experts
+// ascending, then the shared expert), rounding to bf16 after every addition.
 template <int MAXC>
 __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int64_t* ids64,
                                                  const int32_t* __restrict__ inv, const uint16_t* __restrict__ ch,
-                                                 const uint16_t* __restrict__ sh, int T, int H, int E, int k,
-                                                 uint16_t* __restrict__ out) {
+                                                 const float* __restrict__ wf, const uint16_t* __restrict__ wb,
+                                                 const uint16_t* __restrict__ sh, const float* __restrict__ gs,
+                                                 int T, int H, int E, int k, uint16_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   // The token's valid (expert, slot) entries sorted ascending: index_add_ order.
   int ke[16], kr[16], n = 0;
+  float kw[16];
   for (int s = 0; s < k; ++s) {
     const int e = load_id(ids32, ids64, (size_t)t * k + s);
     const int r = inv[(size_t)t * k + s];
     if (e < 0 || e >= E || r < 0) continue;
+    const float w = wf ? wf[(size_t)t * k + s] : bf16_to_f32(wb[(size_t)t * k + s]);
     int pos = n++;
-    while (pos > 0 && ke[pos - 1] > e) { ke[pos] = ke[pos - 1]; kr[pos] = kr[pos - 1]; --pos; }
+    while (pos > 0 && ke[pos - 1] > e) { ke[pos] = ke[pos - 1]; kr[pos] = kr[pos - 1]; kw[pos] = kw[pos - 1]; --pos; }
     ke[pos] = e;
     kr[pos] = r;
+    kw[pos] = w;
   }
   float acc[MAXC][8];
 #pragma unroll
   for (int c = 0; c < MAXC; ++c)
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[c][q] = 0.f;
+  auto add = [&](float* a, const u32x4 v, float w) {
+    const float x[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
+                        bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) a[q] = rbf16(a[q] + rbf16(x[q] * w));
+  };
   for (int j = 0; j < n; ++j) {
     const uint16_t* row = ch + (size_t)kr[j] * H;
+    const float w = kw[j];
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
       const int col = c * 512 + lane * 8;
-      if (col < H) {
-        const u32x4 v = ld16(row + col);
-        acc[c][0] = rbf16(acc[c][0] + bf16_lo(v.x)); acc[c][1] = rbf16(acc[c][1] + bf16_hi(v.x));
-        acc[c][2] = rbf16(acc[c][2] + bf16_lo(v.y)); acc[c][3] = rbf16(acc[c][3] + bf16_hi(v.y));
-        acc[c][4] = rbf16(acc[c][4] + bf16_lo(v.z)); acc[c][5] = rbf16(acc[c][5] + bf16_hi(v.z));
-        acc[c][6] = rbf16(acc[c][6] + bf16_lo(v.w)); acc[c][7] = rbf16(acc[c][7] + bf16_hi(v.w));
-      }
+      if (col < H) add(acc[c], ld16(row + col), w);
     }
   }
+  const float gv = sh ? gs[t] : 0.f;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int col = c * 512 + lane * 8;
     if (col >= H) continue;
-    if (sh) {
-      const u32x4 v = ld16(sh + (size_t)t * H + col);
-      acc[c][0] = rbf16(acc[c][0] + bf16_lo(v.x)); acc[c][1] = rbf16(acc[c][1] + bf16_hi(v.x));
-      acc[c][2] = rbf16(acc[c][2] + bf16_lo(v.y)); acc[c][3] = rbf16(acc[c][3] + bf16_hi(v.y));
-      acc[c][4] = rbf16(acc[c][4] + bf16_lo(v.z)); acc[c][5] = rbf16(acc[c][5] + bf16_hi(v.z));
-      acc[c][6] = rbf16(acc[c][6] + bf16_lo(v.w)); acc[c][7] = rbf16(acc[c][7] + bf16_hi(v.w));
-    }
+    if (sh) add(acc[c], ld16(sh + (size_t)t * H + col), gv);
     u32x4 o;
     o.x = f32_to_bf16(acc[c][0]) | ((uint32_t)f32_to_bf16(acc[c][1]) << 16);
     o.y = f32_to_bf16(acc[c][2]) | ((uint32_t)f32_to_bf16(acc[c][3]) << 16);
@@ -478,9 +905,9 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
 // ---------------------------------------------------------------- driver
 int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, int E, int shared_rows,
                     int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tile_start, uint32_t* status,
-                    hipStream_t s) {
+                    hipStream_t s, int4* desc) {
   hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, s, ids32, ids64, T, k, E, shared_rows, offsets,
-                     tile_start, inv, status);
+                     tile_start, inv, status, desc);
   hipLaunchKernelGGL(k_dispatch_scatter, dim3(E), dim3(1024), 0, s, ids32, ids64, T, k, offsets, perm, inv);
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
@@ -501,7 +928,9 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   uint16_t* act = ws_ptr<uint16_t>(ws, L.act);
   uint16_t* ch = ws_ptr<uint16_t>(ws, L.ch);
   uint16_t* sh = ws_ptr<uint16_t>(ws, L.sh);
-  if (int st = dispatch_launch(ids32, ids64, T, k, E, has_sh ? T : 0, offsets, perm, inv, tile_start, status, s))
+  int4* desc = ws_ptr<int4>(ws, L.desc);
+  if (int st = dispatch_launch(ids32, ids64, T, k, E, has_sh ? T : 0, offsets, perm, inv, tile_start, status, s,
+                               desc))
     return st;
 
   const int n_groups = has_sh ? E + 1 : E;
@@ -510,22 +939,41 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
 
   // One GEMM over groups [lo, hi): bf16 weights, or int4 routed weights (the shared
   // group, always bf16, then gets a launch of its own).
+  // The persistent kernel takes K in whole cycles of kPR stages (H and I multiples of 512),
+  // covers 128 activation columns (up) or 256 output columns (down) per tile and addresses
+  // A rows with 32-bit byte offsets; other shapes take the register-staged kernel (64 and
+  // 128 columns).
+  const int kcyc = kBK * kPR;
+  const bool persistent = H % kcyc == 0 && I % kcyc == 0 && I % kPUpCols == 0 && H % kPDnCols == 0 &&
+                          (size_t)T * H * 2 < ((size_t)1 << 32) && ((size_t)T * k + T) * I * 2 < ((size_t)1 << 32);
+  const int up_cols = persistent ? kPUpCols : 64, dn_cols = persistent ? kPDnCols : 128;
+  static int n_cu[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return TMOE_ERR_HIP;
+  if (!n_cu[dev] && hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return TMOE_ERR_HIP;
+  const unsigned pgrid = (unsigned)(n_cu[dev] >= 8 ? n_cu[dev] / 8 * 8 : 8);
   auto gemm = [&](GemmParams g, int lo, int hi, bool routed_q4, long mchunks) {
     g.group_lo = lo;
     g.group_hi = hi;
     const long grid = (mchunks * g.n_ntiles + 7) / 8 * 8;
-    if (routed_q4)
+    if (persistent && routed_q4)
+      hipLaunchKernelGGL((k_grouped_gemm_p<true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (persistent)
+      hipLaunchKernelGGL((k_grouped_gemm_p<false>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (routed_q4)
       hipLaunchKernelGGL((k_grouped_gemm<kRing, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
     else
       hipLaunchKernelGGL((k_grouped_gemm<kRing, false>), dim3((unsigned)grid), dim3(256), 0, s, g);
   };
   GemmParams up{};
   up.a = x; up.K = H; up.gather = 1; up.offsets = offsets; up.perm = perm; up.tile_start = tile_start;
-  up.T = T; up.E = E; up.k = k; up.n_groups = n_groups; up.n_ntiles = I / 64; up.up = 1; up.N = I; up.I = I;
+  up.T = T; up.E = E; up.k = k; up.n_groups = n_groups; up.n_ntiles = I / up_cols; up.up = 1; up.N = I; up.I = I;
   up.table = table; up.shw0 = sh_gate; up.shw1 = sh_up; up.shared_row0 = T * k; up.out = act;
+  up.desc = desc;
   GemmParams dn = up;
-  dn.a = act; dn.K = I; dn.gather = 0; dn.n_ntiles = H / 128; dn.up = 0; dn.N = H;
-  dn.shw0 = sh_down; dn.shw1 = nullptr; dn.out = ch; dn.out_sh = sh; dn.wf = wf; dn.wb = wb; dn.gs = gs;
+  dn.a = act; dn.K = I; dn.gather = 0; dn.n_ntiles = H / dn_cols; dn.up = 0; dn.N = H;
+  dn.shw0 = sh_down; dn.shw1 = nullptr; dn.out = ch; dn.out_sh = sh;
   if (q4) {
     gemm(up, 0, E, true, mbound);
     if (has_sh) gemm(up, E, E + 1, false, mshared);
@@ -540,10 +988,10 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   const dim3 gc((T + 3) / 4), bc(256);
   const uint16_t* shp = has_sh ? sh : nullptr;
   switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
-    case 2: hipLaunchKernelGGL(k_combine<2>, gc, bc, 0, s, ids32, ids64, inv, ch, shp, T, H, E, k, out); break;
-    case 4: hipLaunchKernelGGL(k_combine<4>, gc, bc, 0, s, ids32, ids64, inv, ch, shp, T, H, E, k, out); break;
-    case 6: hipLaunchKernelGGL(k_combine<6>, gc, bc, 0, s, ids32, ids64, inv, ch, shp, T, H, E, k, out); break;
-    default: hipLaunchKernelGGL(k_combine<8>, gc, bc, 0, s, ids32, ids64, inv, ch, shp, T, H, E, k, out); break;
+    case 2: hipLaunchKernelGGL(k_combine<2>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
+    case 4: hipLaunchKernelGGL(k_combine<4>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
+    case 6: hipLaunchKernelGGL(k_combine<6>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
+    default: hipLaunchKernelGGL(k_combine<8>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
   }
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
@@ -558,5 +1006,5 @@ extern "C" int tmoe_dispatch(const int64_t* ids, int T, int k, int E, int32_t* o
   const Ws L = ws_layout(T, 8, E, 8, k, 0);
   if (ws_bytes < L.scratch + sizeof(int32_t) * (size_t)(E + 64)) return TMOE_ERR_WORKSPACE;
   return dispatch_launch(nullptr, ids, T, k, E, 0, offsets, perm, inv, ws_ptr<int32_t>(workspace, L.scratch),
-                         ws_ptr<uint32_t>(workspace, L.status), (hipStream_t)stream);
+                         ws_ptr<uint32_t>(workspace, L.status), (hipStream_t)stream, nullptr);
 }
