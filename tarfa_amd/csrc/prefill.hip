@@ -177,21 +177,20 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_ca
 // One MFMA B fragment from int4: the 8 weights of 4 packed bytes (byte b = k 2b low
 // nibble, 2b + 1 high nibble), dequantised as bf16((n - 8) * s) -- the reference's
 // `dequant_int4` then bf16 `F.linear` (tarfa/engine/fused_int4.py:258-259).  n * s - 8 s
-// is exact in fp32 (a 4-bit times an 8-bit significand), so one RNE to bf16 reproduces
-// the dequantised matrix bit for bit (finite scales).
-__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return u + 0x7FFFu + ((u >> 16) & 1u);     // bf16 in the high half
-}
+// is exact in fp32 (a 4-bit times an 8-bit significand), so one round-to-nearest-even to
+// bf16 (v_cvt_pk_bf16_f32, two values per instruction) reproduces the dequantised matrix
+// bit for bit (finite scales).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 dequant_frag(uint32_t w, float s) {
   const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
   const float m8 = -8.0f * s;
   uint32_t d[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    const uint32_t e = bf16_rne_bits(fmaf((float)((lo >> (8 * b)) & 0xFFu), s, m8));
-    const uint32_t o = bf16_rne_bits(fmaf((float)((hi >> (8 * b)) & 0xFFu), s, m8));
-    d[b] = __builtin_amdgcn_perm(o, e, 0x07060302u);   // (even k low, odd k high)
+    const float e = fmaf((float)((lo >> (8 * b)) & 0xFFu), s, m8);
+    const float o = fmaf((float)((hi >> (8 * b)) & 0xFFu), s, m8);
+    const bf16x2_t v = {(__bf16)e, (__bf16)o};   // (even k low, odd k high)
+    d[b] = __builtin_bit_cast(uint32_t, v);
   }
   return u32x4{d[0], d[1], d[2], d[3]};
 }
@@ -843,7 +842,8 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 // assignment's expert output and the shared expert's output unscaled (bf16 of the fp32
 // accumulator); this kernel applies the routing weight and the shared gate, each product
 // rounded to bf16, then accumulates in the reference's order (the token's experts
-// ascending, then the shared expert), rounding to bf16 after every addition.
+// ascending, ties in slot order, then the shared expert), rounding to bf16 after every
+// addition.  Lanes 0..k-1 read the token's k entries at once and rank them.
 template <int MAXC>
 __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int64_t* ids64,
                                                  const int32_t* __restrict__ inv, const uint16_t* __restrict__ ch,
@@ -853,38 +853,43 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  // The token's valid (expert, slot) entries sorted ascending: index_add_ order.
-  int ke[16], kr[16], n = 0;
-  float kw[16];
-  for (int s = 0; s < k; ++s) {
-    const int e = load_id(ids32, ids64, (size_t)t * k + s);
-    const int r = inv[(size_t)t * k + s];
-    if (e < 0 || e >= E || r < 0) continue;
-    const float w = wf ? wf[(size_t)t * k + s] : bf16_to_f32(wb[(size_t)t * k + s]);
-    int pos = n++;
-    while (pos > 0 && ke[pos - 1] > e) { ke[pos] = ke[pos - 1]; kr[pos] = kr[pos - 1]; kw[pos] = kw[pos - 1]; --pos; }
-    ke[pos] = e;
-    kr[pos] = r;
-    kw[pos] = w;
+  int e = 0x7FFFFFFF, r = 0;
+  float w = 0.f;
+  bool valid = false;
+  if (lane < k) {
+    const size_t j = (size_t)t * k + lane;
+    e = load_id(ids32, ids64, j);
+    r = inv[j];
+    w = wf ? wf[j] : bf16_to_f32(wb[j]);
+    valid = e >= 0 && e < E && r >= 0;
+    if (!valid) e = 0x7FFFFFFF;
   }
+  int rank = 0;                       // position among the valid entries, by (expert, slot)
+  for (int s2 = 0; s2 < k; ++s2) {
+    const int e2 = __shfl(e, s2);
+    rank += (e2 < e) || (e2 == e && s2 < lane);
+  }
+  const uint64_t vmask = __ballot(valid);
+  const int n = __popcll(vmask);
   float acc[MAXC][8];
 #pragma unroll
   for (int c = 0; c < MAXC; ++c)
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[c][q] = 0.f;
-  auto add = [&](float* a, const u32x4 v, float w) {
+  auto add = [&](float* a, const u32x4 v, float wt) {
     const float x[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
                         bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
 #pragma unroll
-    for (int q = 0; q < 8; ++q) a[q] = rbf16(a[q] + rbf16(x[q] * w));
+    for (int q = 0; q < 8; ++q) a[q] = rbf16(a[q] + rbf16(x[q] * wt));
   };
   for (int j = 0; j < n; ++j) {
-    const uint16_t* row = ch + (size_t)kr[j] * H;
-    const float w = kw[j];
+    const int src = __ffsll((unsigned long long)__ballot(valid && rank == j)) - 1;
+    const uint16_t* row = ch + (size_t)__shfl(r, src) * H;
+    const float wj = __shfl(w, src);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
       const int col = c * 512 + lane * 8;
-      if (col < H) add(acc[c], ld16(row + col), w);
+      if (col < H) add(acc[c], ld16(row + col), wj);
     }
   }
   const float gv = sh ? gs[t] : 0.f;
