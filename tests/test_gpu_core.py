@@ -241,6 +241,35 @@ def test_prefill_group_larger_than_one_tile(gpu):
     assert_close_bf16(f32(out), ref, "skewed prefill")
 
 
+@pytest.mark.parametrize("T,shared", [(1024, True), (700, False)])
+def test_prefill_persistent_gemm_many_tiles(gpu, T, shared):
+    """H and I multiples of 512 take the persistent grouped GEMM (one block per CU walking a
+    tile list with its loads running on across tiles).  1024 tokens x 8 slots over 32 experts
+    is ~256 rows per expert (two M-chunks each: a full one and a partial one), 8 N-tiles per
+    chunk for gate/up and 4 for down: several tiles per block in both GEMMs, so the
+    next-tile prefetch, the epilogue between tiles and the last tile's tail all run."""
+    shape = MoEShape(1024, 32, 1024, 8, 1024 if shared else 0)
+    layer = seeded.make_layer(shape, 60 + T, device=gpu)
+    ws = Workspace(shape, gpu, tokens=T)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    x = seeded.make_tokens(shape, 60 + T, T, device=gpu)
+    logits = seeded.make_logits(shape, 60 + T, T, device=gpu)
+    out, ids, w = tm.moe_block(shape, x, table, ws, logits=logits, shared=layer.shared)
+    ids_ref, w_ref, _ = moe.router_topk(logits.cpu().numpy(), shape.top_k)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    counts = np.bincount(ids_ref.ravel(), minlength=shape.num_experts)
+    assert counts.max() > 160 and (counts % 160 != 0).any()       # multi-chunk groups, partial chunks
+    xs = f32(x)
+    gu, dn = expert_dicts(layer.gate_up, layer.down, ids_ref)
+    ref = moe.experts_prefill(xs, ids_ref, f32(w), gu, dn, shape.num_experts)
+    if shared:
+        ref = moe.add_bf16(ref, moe.shared_expert(xs, *[f32(t) for t in layer.shared]))
+    assert_close_bf16(f32(out), ref, f"persistent prefill T={T}")
+    # the same call again on the same workspace: identical bits
+    out2 = tm.moe_block(shape, x, table, ws, logits=logits, shared=layer.shared)[0]
+    assert torch.equal(out2, out)
+
+
 @pytest.mark.parametrize("E,k", [(32, 8), (256, 8), (8, 8), (16, 4), (512, 8)])
 def test_decode_router_exact_ties(gpu, E, k):
     """The fused decode's in-kernel top-k on supplied logits with many exact ties (and +-0):

@@ -212,12 +212,12 @@ def test_int4_and_bf16_calls_share_a_workspace(gpu):
     ws.status()
 
 
-@pytest.mark.parametrize("T,shared", [(37, True), (300, False), (2, True)])
-def test_int4_prefill_matches_dequantised_bf16_chain(gpu, T, shared):
+@pytest.mark.parametrize("T,shared,I", [(37, True, 512), (300, False, 512), (2, True, 512), (1024, True, 1024)])
+def test_int4_prefill_matches_dequantised_bf16_chain(gpu, T, shared, I):
     """T > 1 in int4 mode: the reference dequantises each hit expert and runs the bf16 prefill
     chain on it (tarfa/engine/fused_int4.py:249-261), so the oracle is experts_prefill on the
     dequantised weights, combined in ascending expert id; the shared expert stays bf16."""
-    shape = MoEShape(1024, 32, 512, 8, 512 if shared else 0)
+    shape = MoEShape(1024, 32, I, 8, I if shared else 0)   # T=1024: several tiles per block
     layer = seeded.make_layer(shape, 40 + T, device=gpu)
     q4 = _q4_layer(layer)
     table = tm.expert_table_q4(*q4)
