@@ -15,6 +15,7 @@
  *     and not written by the caller afterwards: the kernels return its counters
  *     to zero and keep a call counter (epoch) in it.  Calls that share one
  *     workspace must be ordered (same stream, or joined with events).
+ *   - T > 1 (dispatch and the prefill paths): T*k <= 524288.
  *   - Expert weights are reached through a device "expert table":
  *       bf16 table  uint64_t[E][2] = { gate_up [2I, H], down [H, I] } base pointers
  *       int4 table  uint64_t[E][4] = { gate_up packed [2I, H/2] u8, gate_up scales

@@ -70,11 +70,19 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, c
   __syncthreads();
   const int n = T * k;
   bool bad = false;
-  for (int j = tid; j < n; j += 1024) {
-    const int e = load_id(ids32, ids64, j);
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-    else if (e != E) bad = true;
-    inv[j] = -1;
+  for (int j0 = tid; j0 < n; j0 += 8 * 1024) {       // 8 independent loads in flight per thread
+    int ev[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) ev[u] = j0 + u * 1024 < n ? load_id(ids32, ids64, j0 + u * 1024) : E;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u * 1024;
+      if (j >= n) continue;
+      const int e = ev[u];
+      if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+      else if (e != E) bad = true;
+      inv[j] = -1;
+    }
   }
   if (bad && status) atomicOr(status + kStatusError, 1u);
   __syncthreads();
@@ -116,40 +124,57 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, c
 }
 
 // One block per expert: stable compaction of the slot-major traversal j = slot*T + t.
+// The block reads the ids once in memory order (i = t*k + slot, coalesced) and marks its
+// expert's entries in an LDS bitmask indexed by j; thread i then owns the whole words
+// [i wpt, (i + 1) wpt) of the mask: it counts their bits, one block-wide exclusive scan
+// gives its first position, and it writes perm and inv for its set bits in j order.
+constexpr int kScatterMaxN = 1 << 19;   // T*k up to 512 Ki entries (a 64 KB mask)
 __global__ __launch_bounds__(1024) void k_dispatch_scatter(const int32_t* ids32, const int64_t* ids64, int T, int k,
                                                            const int32_t* __restrict__ offsets, int32_t* perm,
                                                            int32_t* inv) {
+  __shared__ uint32_t mask[kScatterMaxN / 32];
   __shared__ int wave_tot[16];
   const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int n = T * k;
-  int running = offsets[e];
-  for (int j0 = 0; j0 < n; j0 += 1024) {
-    const int j = j0 + tid;
-    int slot = 0, t = 0;
-    bool match = false;
-    if (j < n) {
-      slot = j / T;
-      t = j - slot * T;
-      match = load_id(ids32, ids64, (size_t)t * k + slot) == e;
-    }
-    const uint64_t mask = __ballot(match);
-    const int before = __popcll(mask & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_tot[wid] = __popcll(mask);
-    __syncthreads();
-    int wofs = 0, total = 0;
+  const int nw = (n + 31) / 32;
+  for (int w = tid; w < nw; w += 1024) mask[w] = 0u;
+  __syncthreads();
+  for (int i0 = tid; i0 < n; i0 += 8 * 1024) {       // 8 independent loads in flight per thread
+    int ev[8];
 #pragma unroll
-    for (int w = 0; w < 16; ++w) {
-      const int v = wave_tot[w];
-      wofs += w < wid ? v : 0;
-      total += v;
+    for (int u = 0; u < 8; ++u) ev[u] = i0 + u * 1024 < n ? load_id(ids32, ids64, i0 + u * 1024) : -1;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (ev[u] != e) continue;
+      const int i = i0 + u * 1024, t = i / k, slot = i - t * k, j = slot * T + t;
+      atomicOr(&mask[j >> 5], 1u << (j & 31));
     }
-    if (match) {
-      const int r = running + wofs + before;
+  }
+  __syncthreads();
+  const int wpt = (nw + 1023) / 1024;
+  const int w_lo = min(nw, tid * wpt), w_hi = min(nw, w_lo + wpt);
+  int c = 0;
+  for (int w = w_lo; w < w_hi; ++w) c += __popc(mask[w]);
+  // Block-wide exclusive scan of c: inclusive within the wave, then the waves' totals.
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int v = __shfl_up(incl, d);
+    if (lane >= d) incl += v;
+  }
+  if (lane == 63) wave_tot[wid] = incl;
+  __syncthreads();
+  int before = incl - c;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) before += w < wid ? wave_tot[w] : 0;
+  int r = offsets[e] + before;
+  for (int w = w_lo; w < w_hi && c > 0; ++w) {
+    for (uint32_t m = mask[w]; m; m &= m - 1) {
+      const int j = 32 * w + __ffs(m) - 1, slot = j / T, t = j - slot * T;
       perm[r] = t * k + slot;
       inv[(size_t)t * k + slot] = r;
+      ++r;
     }
-    running += total;
-    __syncthreads();
   }
 }
 
@@ -911,6 +936,7 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
 int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, int E, int shared_rows,
                     int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tile_start, uint32_t* status,
                     hipStream_t s, int4* desc) {
+  if ((long)T * k > kScatterMaxN) return TMOE_ERR_SHAPE;
   hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, s, ids32, ids64, T, k, E, shared_rows, offsets,
                      tile_start, inv, status, desc);
   hipLaunchKernelGGL(k_dispatch_scatter, dim3(E), dim3(1024), 0, s, ids32, ids64, T, k, offsets, perm, inv);

@@ -185,7 +185,7 @@ def test_decode_workspace_reuse_and_epoch_wrap(gpu):
     ws.status()
 
 
-@pytest.mark.parametrize("T,E,k", [(4096, 256, 8), (5, 32, 8), (1000, 16, 1), (300, 4, 2)])
+@pytest.mark.parametrize("T,E,k", [(4096, 256, 8), (5, 32, 8), (1000, 16, 1), (300, 4, 2), (20000, 64, 8)])
 def test_dispatch_bit_exact(gpu, T, E, k):
     g = np.random.default_rng(T + E)
     ids = np.stack([g.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
@@ -200,6 +200,15 @@ def test_dispatch_bit_exact(gpu, T, E, k):
     inv_ref = np.full(T * k, -1, np.int64)
     inv_ref[p_ref] = np.arange(n)
     assert np.array_equal(inv.cpu().numpy(), inv_ref)
+
+
+def test_dispatch_rejects_too_many_entries(gpu):
+    """T*k above 524288 (the scatter's LDS mask) is refused before any launch."""
+    T, k, E = 65537, 8, 16
+    ids = torch.zeros(T, k, dtype=torch.int64, device=gpu)
+    ws = Workspace(MoEShape(128, E, 64, k), gpu, tokens=T)
+    with pytest.raises(RuntimeError, match="unsupported or inconsistent sizes"):
+        tm.dispatch(ids, E, ws)
 
 
 @pytest.mark.parametrize("T,shared", [(2, False), (37, True), (300, True)])
