@@ -869,7 +869,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 // rounded to bf16, then accumulates in the reference's order (the token's experts
 // ascending, ties in slot order, then the shared expert), rounding to bf16 after every
 // addition.  Lanes 0..k-1 read the token's k entries at once and rank them.
-template <int MAXC>
+template <int MAXC, int MAXK>
 __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int64_t* ids64,
                                                  const int32_t* __restrict__ inv, const uint16_t* __restrict__ ch,
                                                  const float* __restrict__ wf, const uint16_t* __restrict__ wb,
@@ -907,22 +907,30 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
 #pragma unroll
     for (int q = 0; q < 8; ++q) a[q] = rbf16(a[q] + rbf16(x[q] * wt));
   };
-  for (int j = 0; j < n; ++j) {
-    const int src = __ffsll((unsigned long long)__ballot(valid && rank == j)) - 1;
-    const uint16_t* row = ch + (size_t)__shfl(r, src) * H;
-    const float wj = __shfl(w, src);
+  // The entries in rank order (wave-uniform), then per chunk every row's load issued before
+  // the additions, which stay in rank order.
+  int rows[MAXK];
+  float wr[MAXK];
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int col = c * 512 + lane * 8;
-      if (col < H) add(acc[c], ld16(row + col), wj);
-    }
+  for (int j = 0; j < MAXK; ++j) {
+    const int src = __ffsll((unsigned long long)__ballot(valid && rank == j)) - 1;
+    rows[j] = j < n ? __shfl(r, src) : 0;
+    wr[j] = j < n ? __shfl(w, src) : 0.f;
   }
   const float gv = sh ? gs[t] : 0.f;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int col = c * 512 + lane * 8;
     if (col >= H) continue;
-    if (sh) add(acc[c], ld16(sh + (size_t)t * H + col), gv);
+    u32x4 v[MAXK];
+#pragma unroll
+    for (int j = 0; j < MAXK; ++j)
+      if (j < n) v[j] = ld16(ch + (size_t)rows[j] * H + col);
+    const u32x4 vs = sh ? ld16(sh + (size_t)t * H + col) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < MAXK; ++j)
+      if (j < n) add(acc[c], v[j], wr[j]);
+    if (sh) add(acc[c], vs, gv);
     u32x4 o;
     o.x = f32_to_bf16(acc[c][0]) | ((uint32_t)f32_to_bf16(acc[c][1]) << 16);
     o.y = f32_to_bf16(acc[c][2]) | ((uint32_t)f32_to_bf16(acc[c][3]) << 16);
@@ -1018,11 +1026,20 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   const int nc = (H + 511) / 512;
   const dim3 gc((T + 3) / 4), bc(256);
   const uint16_t* shp = has_sh ? sh : nullptr;
-  switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
-    case 2: hipLaunchKernelGGL(k_combine<2>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
-    case 4: hipLaunchKernelGGL(k_combine<4>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
-    case 6: hipLaunchKernelGGL(k_combine<6>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
-    default: hipLaunchKernelGGL(k_combine<8>, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out); break;
+  auto combine = [&](auto kern) {
+    hipLaunchKernelGGL(kern, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out);
+  };
+  const int mc = nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8;
+  if (k <= 8) {
+    if (mc == 2) combine(k_combine<2, 8>);
+    else if (mc == 4) combine(k_combine<4, 8>);
+    else if (mc == 6) combine(k_combine<6, 8>);
+    else combine(k_combine<8, 8>);
+  } else {
+    if (mc == 2) combine(k_combine<2, 16>);
+    else if (mc == 4) combine(k_combine<4, 16>);
+    else if (mc == 6) combine(k_combine<6, 16>);
+    else combine(k_combine<8, 16>);
   }
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
