@@ -168,6 +168,29 @@ int tmoe_moe_block_int4(const void* x, int T, const void* router_w, const float*
                         int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                         void* workspace, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- the MoE sublayer
+ * The steps on either side of the block in a Qwen3.5-MoE decoder layer
+ * (transformers/models/qwen3_5_moe/modeling_qwen3_5_moe.py:870-875): h is the hidden
+ * state before the post-attention RMSNorm (:801-818) and
+ *   x   = bf16(h * (1 / sqrt(mean(h^2) + eps)) * (1 + ln_w))   (fp32 arithmetic)
+ *   out = bf16(h + moe_block(x))
+ * with moe_block exactly tmoe_moe_block_bf16 / _int4 on x.  ln_w [H] bf16 (the
+ * zero-centred weight: the scale is 1 + ln_w); eps >= 0; out must not alias h.
+ * Batch 1 on the fused decode kernel forms x in each of its tasks and adds h in its
+ * combine (no extra launch); T > 1 normalises once (workspace) and adds h in the
+ * prefill combine.  Arguments otherwise as tmoe_moe_block_bf16 / _int4.
+ */
+int tmoe_moe_layer_bf16(const void* h, int T, const void* ln_w, float eps, const void* router_w,
+                        const float* logits_in, const uint64_t* expert_table, const void* sh_gate,
+                        const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E, int I,
+                        int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                        void* workspace, size_t ws_bytes, void* stream);
+int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float eps, const void* router_w,
+                        const float* logits_in, const uint64_t* expert_table_q4, const void* sh_gate,
+                        const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E, int I,
+                        int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                        void* workspace, size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------- route telemetry (a13)
  * The reference's per-layer route-reuse counters (tarfa/engine/fused_int4.py:71-95
  * _record_route / routing_telemetry), kept on the device so decode never synchronises

@@ -202,3 +202,23 @@ def moe_block(x, logits_or_wg, k, gate_up, down, num_experts, shared=None, logit
     if shared is not None:
         routed = add_bf16(routed, shared_expert(x, *shared))
     return routed, ids, w
+
+
+# ---------------------------------------------------------------- the sublayer around the block
+
+def rmsnorm(h, w, eps):
+    """Qwen3_5MoeRMSNorm (transformers modeling_qwen3_5_moe.py:800-814, applied at :870):
+    in fp32, y = h * rsqrt(mean(h^2) + eps), then bf16(y * (1 + w)).  The mean is taken in
+    fp64 and rounded to fp32 (the value every fp32 summation order approximates); rsqrt as
+    1 / sqrt, each step rounded to fp32."""
+    h = np.asarray(h, np.float32)
+    w = np.asarray(w, np.float32)
+    ms = np.mean(np.asarray(h, np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    rs = (np.float32(1.0) / np.sqrt(ms + np.float32(eps))).astype(np.float32)
+    y = (h * rs).astype(np.float32)
+    return rb((y * (np.float32(1.0) + w)).astype(np.float32))
+
+
+def moe_layer(h, block_out):
+    """The residual add after the block (transformers modeling_qwen3_5_moe.py:875): bf16(h + y)."""
+    return add_bf16(h, block_out)

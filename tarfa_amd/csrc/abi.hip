@@ -14,8 +14,10 @@ int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64,
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s, bool q4);
+                   void* ws, hipStream_t s, bool q4, const uint16_t* resid);
 int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
+int rmsnorm_launch(const uint16_t* h, const uint16_t* w, float eps, int T, int H, uint16_t* x, hipStream_t s);
+int residual_add_launch(const uint16_t* h, uint16_t* y, size_t n, hipStream_t s);
 }  // namespace tmoe
 
 
@@ -121,7 +123,7 @@ static int experts_forward(const void* x, int T, const int64_t* ids, const void*
     return q4 ? decode_fused_launch(p, false, s) : decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
-                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4);
+                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4, nullptr);
 }
 
 extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
@@ -138,15 +140,20 @@ extern "C" int tmoe_experts_forward_int4(const void* x, int T, const int64_t* id
                          (hipStream_t)stream, true);
 }
 
+// ln_w non-null: x is the hidden state h before the layer's RMSNorm; the block runs on
+// bf16(rmsnorm(h) * (1 + ln_w)) and out = bf16(h + block output).
 static int moe_block(const void* x, int T, const void* router_w, const float* logits_in, const uint64_t* expert_table,
                      const void* sh_gate, const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E,
                      int I, int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
-                     void* workspace, size_t ws_bytes, hipStream_t s, bool q4) {
+                     void* workspace, size_t ws_bytes, hipStream_t s, bool q4, const void* ln_w = nullptr,
+                     float ln_eps = 0.f) {
   const bool has_sh = sh_gate || sh_up || sh_down || sh_gate_w;
   if (has_sh && (!sh_gate || !sh_up || !sh_down || !sh_gate_w || Is < 8)) return TMOE_ERR_NULL;
   if (!has_sh) Is = 0;
   if (int st = check_shape(T, H, E, I, k, Is)) return st;
   if (!x || !expert_table || !out || !workspace || (!router_w && !logits_in)) return TMOE_ERR_NULL;
+  if (ln_w && (misaligned(ln_w) || misaligned(out))) return TMOE_ERR_ALIGN;
+  if (ln_w && (out == x || !(ln_eps >= 0.f))) return TMOE_ERR_SHAPE;
   if (misaligned(x) || misaligned(workspace) || (router_w && misaligned(router_w)) ||
       (has_sh && (misaligned(sh_gate) || misaligned(sh_up) || misaligned(sh_down) || misaligned(sh_gate_w))))
     return TMOE_ERR_ALIGN;
@@ -170,9 +177,29 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     p.w_out = (uint16_t*)weights_out;
     p.heat = heat;
     bind_ws(p, workspace, ws_bytes, L);
-    return q4 ? decode_fused_launch(p, true, s) : decode(p, true, s);
+    if (!ln_w) return q4 ? decode_fused_launch(p, true, s) : decode(p, true, s);
+    // The fused kernel forms the normalised input in every task and adds the residual in
+    // its combine; other shapes normalise first and add the residual after.
+    p.ln_w = (const uint16_t*)ln_w;
+    p.ln_eps = ln_eps;
+    p.resid = (const uint16_t*)x;
+    const int st = decode_fused_launch(p, true, s);
+    if (st != TMOE_ERR_SHAPE || q4) return st;
+    uint16_t* xn = ws_ptr<uint16_t>(workspace, L.xn);
+    if (int st2 = rmsnorm_launch((const uint16_t*)x, (const uint16_t*)ln_w, ln_eps, 1, H, xn, s)) return st2;
+    p.x = xn;
+    p.ln_w = nullptr;
+    p.resid = nullptr;
+    if (int st2 = decode(p, true, s)) return st2;
+    return residual_add_launch((const uint16_t*)x, (uint16_t*)out, (size_t)H, s);
   }
   // T > 1: router, shared gate, then the prefill experts path with the shared expert as an extra group.
+  const void* h = x;
+  if (ln_w) {
+    uint16_t* xn = ws_ptr<uint16_t>(workspace, L.xn);
+    if (int st = rmsnorm_launch((const uint16_t*)h, (const uint16_t*)ln_w, ln_eps, T, H, xn, s)) return st;
+    x = xn;
+  }
   float* logits = ws_ptr<float>(workspace, L.logits);
   int32_t* ids32 = ws_ptr<int32_t>(workspace, L.ids);
   float* wf = ws_ptr<float>(workspace, L.wts);
@@ -187,7 +214,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     if (int st = launch_shared_gate((const uint16_t*)x, (const uint16_t*)sh_gate_w, T, H, gs, s)) return st;
   return prefill_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
                         (const uint16_t*)sh_up, (const uint16_t*)sh_down, has_sh ? gs : nullptr, H, E, I, k, Is,
-                        (uint16_t*)out, workspace, s, q4);
+                        (uint16_t*)out, workspace, s, q4, ln_w ? (const uint16_t*)h : nullptr);
 }
 
 extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,
@@ -206,4 +233,25 @@ extern "C" int tmoe_moe_block_int4(const void* x, int T, const void* router_w, c
                                    void* workspace, size_t ws_bytes, void* stream) {
   return moe_block(x, T, router_w, logits_in, expert_table_q4, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
                    out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, true);
+}
+
+// The MoE sublayer of a decoder layer: out = bf16(h + block(bf16(rmsnorm(h) * (1 + ln_w)))).
+extern "C" int tmoe_moe_layer_bf16(const void* h, int T, const void* ln_w, float eps, const void* router_w,
+                                   const float* logits_in, const uint64_t* expert_table, const void* sh_gate,
+                                   const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E, int I,
+                                   int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  if (!ln_w) return TMOE_ERR_NULL;
+  return moe_block(h, T, router_w, logits_in, expert_table, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, out,
+                   ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, false, ln_w, eps);
+}
+
+extern "C" int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float eps, const void* router_w,
+                                   const float* logits_in, const uint64_t* expert_table_q4, const void* sh_gate,
+                                   const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E, int I,
+                                   int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  if (!ln_w) return TMOE_ERR_NULL;
+  return moe_block(h, T, router_w, logits_in, expert_table_q4, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
+                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, true, ln_w, eps);
 }

@@ -205,10 +205,11 @@ constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
 // SwiGLU of gate/up row pairs [i0, i0 + P): P / 2 tagged activation pairs.
 template <int MH, bool EXACT, int P, typename Take>
 __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* up, int i0, int n_rows, int K,
-                                         const uint16_t* x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
+                                         const uint16_t* x, const uint16_t* ln_w, float eps, int lane, uint64_t* act64,
+                                         uint32_t tag, Take&& take) {
   static_assert(P % 2 == 0, "activations are published as tagged bf16 pairs");
   XPack<MH> xf;
-  load_xpack<MH, EXACT>(xf, x, K, lane);
+  load_x<MH, EXACT>(xf, x, ln_w, eps, K, lane);
   const uint16_t* rows[2 * P];
 #pragma unroll
   for (int q = 0; q < P; ++q) {
@@ -264,12 +265,13 @@ __device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act
 // tagged bf16 pairs.  Loads in need order: input, scales, then the 2R weight rows.
 template <int MH, int R, typename Take>
 __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int i0, int I, int H,
-                                      const uint16_t* x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
+                                      const uint16_t* x, const uint16_t* ln_w, float eps, int lane, uint64_t* act64,
+                                      uint32_t tag, Take&& take) {
   constexpr int G = 4 * MH;            // scale groups per row (H = 512 MH)
   constexpr int NW = R * G / 2;        // scale words of R rows
   static_assert(R % 2 == 0 && NW <= 128, "scale words of a block fit two per lane");
   XPack<MH> xf;
-  load_xpack<MH, true>(xf, x, H, lane);
+  load_x<MH, true>(xf, x, ln_w, eps, H, lane);
   // Scale words of the R gate rows and of the R up rows: word i of a block in lane i % 64, register i / 64.
   const uint32_t* sg = reinterpret_cast<const uint32_t*>(gs + (size_t)i0 * G);
   const uint32_t* su = reinterpret_cast<const uint32_t*>(gs + (size_t)(I + i0) * G);
@@ -636,7 +638,7 @@ __device__ __forceinline__ void task_router(const DecodeParams& p, int t, int la
   const int r0 = t * kRouterRows;
   if (r0 >= n_rows) return;
   XPack<MH> xf;
-  load_xpack<MH, EXACT>(xf, p.x, p.H, lane);
+  load_x<MH, EXACT>(xf, p.x, p.ln_w, p.ln_eps, p.H, lane);
   const uint16_t* rp[kRouterRows];
 #pragma unroll
   for (int r = 0; r < kRouterRows; ++r) {
@@ -722,6 +724,7 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
     for (int j = 1; j < kFusedMaxK; ++j) ps = j == k - 1 ? pr[j] : ps;
     acc = rbf16(acc + rbf16(g * ((r & 1) ? bf16_hi(ps) : bf16_lo(ps))));
   }
+  if (p.resid && lane < kDownRows) acc = bf16_to_f32(p.resid[h0 + lane]) + acc;   // the layer's residual add
   if (lane < kDownRows) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
@@ -779,6 +782,7 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
     for (int j = 1; j < kFusedMaxK; ++j) ps = j == k - 1 ? pr[j] : ps;
     acc = rbf16(acc + rbf16(g * __uint_as_float(ps)));
   }
+  if (p.resid && lane < RQ) acc = bf16_to_f32(p.resid[h0 + lane]) + acc;   // the layer's residual add
   if (lane < RQ) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
@@ -855,10 +859,17 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
   }
 }
 
-// Q4: routed experts in int4 (table [E][4]); the shared expert stays bf16.
-template <int MH, int MI, bool EXACT, bool Q4>
+// Q4: routed experts in int4 (table [E][4]); the shared expert stays bf16.  LN: the input
+// is the hidden state before the layer's RMSNorm (every task that loads x forms it) and
+// the combine adds the residual; without LN both pointers are null constants here, so
+// none of that code is in the kernel.
+template <int MH, int MI, bool EXACT, bool Q4, bool LN>
 __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   static_assert(!Q4 || EXACT, "int4 variants need H and I multiples of 512");
+  if constexpr (!LN) {
+    p.ln_w = nullptr;
+    p.resid = nullptr;
+  }
   constexpr int RQ = q4_down_rows(MI);
   const int lane0 = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -938,13 +949,13 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         if (e >= 0)
           up_q4<MH, kQ4Pairs>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 1)), tk.idx * kQ4Pairs, p.I, p.H,
-                    p.x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag, take);
+                    p.x, p.ln_w, p.ln_eps, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag, take);
       } else if (e >= 0) {
         const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
         const uint16_t* g = shared ? p.sh_gate : gu;
         const uint16_t* u = shared ? p.sh_up : gu + (size_t)p.I * p.H;
         constexpr int P = Q4 ? kQ4SPairs : kPairs;
-        up_pairs<MH, EXACT, P>(g, u, tk.idx * P, n_rows, p.H, p.x, lane,
+        up_pairs<MH, EXACT, P>(g, u, tk.idx * P, n_rows, p.H, p.x, p.ln_w, p.ln_eps, lane,
                             p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag, take);
       }
     } else if (Q4 && tk.type == kTD) {
@@ -1009,28 +1020,29 @@ typedef void (*FusedKernel)(DecodeParams);
 // Exact-fit variants (H = 512 MH, I = Is = 512 MI) for the common layer widths;
 // masked variants cover the rest up to H = 4096, I = Is = 2048.
 // Int4 mode has exact-fit variants only.
-static FusedKernel pick_fused(int H, int I, int Is, bool q4) {
+template <bool LN>
+static FusedKernel pick_fused_t(int H, int I, int Is, bool q4) {
   if (H % 512 == 0 && I % 512 == 0 && (Is == 0 || Is == I)) {
     const int key = (H / 512) * 10 + I / 512;
     if (q4) {
       switch (key) {
-        case 11: return k_decode_fused<1, 1, true, true>;
-        case 21: return k_decode_fused<2, 1, true, true>;
-        case 22: return k_decode_fused<2, 2, true, true>;
-        case 42: return k_decode_fused<4, 2, true, true>;
-        case 52: return k_decode_fused<5, 2, true, true>;
-        case 62: return k_decode_fused<6, 2, true, true>;
-        case 84: return k_decode_fused<8, 4, true, true>;
+        case 11: return k_decode_fused<1, 1, true, true, LN>;
+        case 21: return k_decode_fused<2, 1, true, true, LN>;
+        case 22: return k_decode_fused<2, 2, true, true, LN>;
+        case 42: return k_decode_fused<4, 2, true, true, LN>;
+        case 52: return k_decode_fused<5, 2, true, true, LN>;
+        case 62: return k_decode_fused<6, 2, true, true, LN>;
+        case 84: return k_decode_fused<8, 4, true, true, LN>;
       }
       return nullptr;
     }
     switch (key) {
-      case 21: return k_decode_fused<2, 1, true, false>;
-      case 22: return k_decode_fused<2, 2, true, false>;
-      case 42: return k_decode_fused<4, 2, true, false>;
-      case 52: return k_decode_fused<5, 2, true, false>;
-      case 62: return k_decode_fused<6, 2, true, false>;
-      case 84: return k_decode_fused<8, 4, true, false>;
+      case 21: return k_decode_fused<2, 1, true, false, LN>;
+      case 22: return k_decode_fused<2, 2, true, false, LN>;
+      case 42: return k_decode_fused<4, 2, true, false, LN>;
+      case 52: return k_decode_fused<5, 2, true, false, LN>;
+      case 62: return k_decode_fused<6, 2, true, false, LN>;
+      case 84: return k_decode_fused<8, 4, true, false, LN>;
     }
   }
   if (q4) return nullptr;
@@ -1039,16 +1051,19 @@ static FusedKernel pick_fused(int H, int I, int Is, bool q4) {
   const int mh = ncH <= 2 ? 2 : ncH <= 4 ? 4 : ncH <= 6 ? 6 : ncH <= 8 ? 8 : 0;
   const int mi = ncI <= 2 ? 2 : ncI <= 4 ? 4 : 0;
   switch (mh * 10 + mi) {
-    case 22: return k_decode_fused<2, 2, false, false>;
-    case 24: return k_decode_fused<2, 4, false, false>;
-    case 42: return k_decode_fused<4, 2, false, false>;
-    case 44: return k_decode_fused<4, 4, false, false>;
-    case 62: return k_decode_fused<6, 2, false, false>;
-    case 64: return k_decode_fused<6, 4, false, false>;
-    case 82: return k_decode_fused<8, 2, false, false>;
-    case 84: return k_decode_fused<8, 4, false, false>;
+    case 22: return k_decode_fused<2, 2, false, false, LN>;
+    case 24: return k_decode_fused<2, 4, false, false, LN>;
+    case 42: return k_decode_fused<4, 2, false, false, LN>;
+    case 44: return k_decode_fused<4, 4, false, false, LN>;
+    case 62: return k_decode_fused<6, 2, false, false, LN>;
+    case 64: return k_decode_fused<6, 4, false, false, LN>;
+    case 82: return k_decode_fused<8, 2, false, false, LN>;
+    case 84: return k_decode_fused<8, 4, false, false, LN>;
   }
   return nullptr;
+}
+static FusedKernel pick_fused(int H, int I, int Is, bool q4, bool ln) {
+  return ln ? pick_fused_t<true>(H, I, Is, q4) : pick_fused_t<false>(H, I, Is, q4);
 }
 
 // Blocks of a kernel to launch on the current device (cached): every one resident
@@ -1077,7 +1092,7 @@ static int resident_blocks(FusedKernel k) {
 
 int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   const bool has_sh = p.sh_gate != nullptr;
-  FusedKernel k = pick_fused(p.H, p.I, p.Is, p.q4 != 0);
+  FusedKernel k = pick_fused(p.H, p.I, p.Is, p.q4 != 0, p.ln_w != nullptr);
   if (!k || p.k > kFusedMaxK || (has_sh && !run_router) || (p.I & 1) || (p.Is & 1) || (p.H % kDownRows))
     return TMOE_ERR_SHAPE;
   const int n_rows = (p.logits_in ? 0 : p.E) + (has_sh ? 1 : 0);

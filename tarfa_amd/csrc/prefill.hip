@@ -874,7 +874,8 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
                                                  const int32_t* __restrict__ inv, const uint16_t* __restrict__ ch,
                                                  const float* __restrict__ wf, const uint16_t* __restrict__ wb,
                                                  const uint16_t* __restrict__ sh, const float* __restrict__ gs,
-                                                 int T, int H, int E, int k, uint16_t* __restrict__ out) {
+                                                 const uint16_t* __restrict__ resid, int T, int H, int E, int k,
+                                                 uint16_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -931,6 +932,13 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
     for (int j = 0; j < MAXK; ++j)
       if (j < n) add(acc[c], v[j], wr[j]);
     if (sh) add(acc[c], vs, gv);
+    if (resid) {   // the layer's residual add: bf16(h + y)
+      const u32x4 hv = ld16(resid + (size_t)t * H + col);
+      const float hx[8] = {bf16_lo(hv.x), bf16_hi(hv.x), bf16_lo(hv.y), bf16_hi(hv.y),
+                           bf16_lo(hv.z), bf16_hi(hv.z), bf16_lo(hv.w), bf16_hi(hv.w)};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[c][q] = hx[q] + acc[c][q];
+    }
     u32x4 o;
     o.x = f32_to_bf16(acc[c][0]) | ((uint32_t)f32_to_bf16(acc[c][1]) << 16);
     o.y = f32_to_bf16(acc[c][2]) | ((uint32_t)f32_to_bf16(acc[c][3]) << 16);
@@ -954,7 +962,7 @@ int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, in
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s, bool q4) {
+                   void* ws, hipStream_t s, bool q4, const uint16_t* resid) {
   const bool has_sh = sh_gate != nullptr;
   if (H % 128 || I % 64 || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
   if (q4 && I % 128) return TMOE_ERR_SHAPE;   // int4: every 64-wide K stage inside one 128-column group
@@ -1027,7 +1035,7 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   const dim3 gc((T + 3) / 4), bc(256);
   const uint16_t* shp = has_sh ? sh : nullptr;
   auto combine = [&](auto kern) {
-    hipLaunchKernelGGL(kern, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, T, H, E, k, out);
+    hipLaunchKernelGGL(kern, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, resid, T, H, E, k, out);
   };
   const int mc = nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8;
   if (k <= 8) {

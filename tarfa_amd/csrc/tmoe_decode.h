@@ -6,7 +6,10 @@
 namespace tmoe {
 
 struct DecodeParams {
-  const uint16_t* x;          // [H]
+  const uint16_t* x;          // [H]; with ln_w: the hidden state h before the layer's RMSNorm
+  const uint16_t* ln_w;       // [H] RMSNorm weight (x := bf16(rmsnorm(h) * (1 + ln_w))), or null
+  float ln_eps;
+  const uint16_t* resid;      // [H] residual added to the output (out = bf16(resid + y)), or null
   const uint16_t* router_w;   // [E, H] or null (logits supplied or experts-only mode)
   const float* logits_in;     // [E] or null
   const uint64_t* table;      // [E][2] gate_up / down base pointers; int4: [E][4] (packed, scales) x 2

@@ -68,6 +68,58 @@ __device__ __forceinline__ void load_xpack(XPack<MAXC>& f, const uint16_t* __res
   }
 }
 
+// The fragment of x = RMSNorm(h) instead (transformers modeling_qwen3_5_moe.py:806-814):
+// in fp32, y = h * (1 / sqrt(mean(h^2) + eps)), then bf16(y * (1 + w)).  The squares are
+// rounded and summed per lane in element order, then across the wave by an xor butterfly
+// (every lane ends with the same bits), so every wave that loads it gets the same x.
+template <int MAXC, bool EXACT>
+__device__ __forceinline__ void load_xpack_norm(XPack<MAXC>& f, const uint16_t* __restrict__ h,
+                                                const uint16_t* __restrict__ w, float eps, int K, int lane) {
+  u32x4 hv[MAXC], wv[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int col = c * 512 + lane * 8;
+    const bool in = EXACT || col < K;
+    hv[c] = in ? ld16(h + col) : u32x4{0u, 0u, 0u, 0u};
+    wv[c] = in ? ld16(w + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const uint32_t q[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = bf16_lo(q[i]), b = bf16_hi(q[i]);
+      ss = __fadd_rn(ss, __fmul_rn(a, a));
+      ss = __fadd_rn(ss, __fmul_rn(b, b));
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, d));
+  const float rs = 1.0f / sqrtf(__fadd_rn(ss / (float)K, eps));
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const uint32_t q[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+    const uint32_t g[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = __fmul_rn(__fmul_rn(bf16_lo(q[i]), rs), __fadd_rn(1.0f, bf16_lo(g[i])));
+      const float hi = __fmul_rn(__fmul_rn(bf16_hi(q[i]), rs), __fadd_rn(1.0f, bf16_hi(g[i])));
+      o[i] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    }
+    f.v[c] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// x, or RMSNorm(h) when a norm weight is given.
+template <int MAXC, bool EXACT>
+__device__ __forceinline__ void load_x(XPack<MAXC>& f, const uint16_t* x, const uint16_t* ln_w, float eps, int K,
+                                       int lane) {
+  if (ln_w) load_xpack_norm<MAXC, EXACT>(f, x, ln_w, eps, K, lane);
+  else load_xpack<MAXC, EXACT>(f, x, K, lane);
+}
+
 // Dots of R weight rows with a packed fragment (v_dot2 bf16, fp32 accumulation);
 // all R x MAXC 16-byte loads are issued before any arithmetic.  Every lane gets the sums.
 template <int MAXC, int R, bool EXACT>

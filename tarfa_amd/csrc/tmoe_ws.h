@@ -58,6 +58,7 @@ struct Ws {
   size_t scratch;  // int32[E + 64]      dispatch counters
   size_t ch;       // bf16[T * k * H]    per-assignment expert outputs, unscaled (T > 1)
   size_t desc;     // int32x4[T * k / 64 + E + T / 64 + 2]   prefill M-chunk descriptors (T > 1)
+  size_t xn;       // bf16[T * H]        RMSNorm of the hidden state (the layer entry points)
   size_t tagged;   // u64[kLogitReplicas * logit_stride(E) + (k * I + Is) / 2 + (k + 1) * H]  tagged
                    // logit copies, activation pairs, per-slot down results (slot k = shared expert)
   size_t total;
@@ -85,6 +86,7 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.scratch = take(sizeof(int32_t) * (size_t)(E + 64));
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
   w.desc = take(t > 1 ? 16 * (t * (size_t)k / 64 + (size_t)E + t / 64 + 2) : 0);
+  w.xn = take(2 * t * (size_t)H);
   w.tagged = take(8 * ((size_t)kLogitReplicas * logit_stride(E) + ((size_t)k * I + (size_t)Is) / 2 +
                         (size_t)(k + 1) * H));
   w.total = o;

@@ -192,8 +192,16 @@ def experts_forward(shape: MoEShape, x, ids, weights, table, workspace: Workspac
     return out
 
 
+def moe_layer(shape: MoEShape, h, ln_w, eps, table, workspace: Workspace, **kw):
+    """The MoE sublayer of a decoder layer: bf16(h + moe_block(rmsnorm(h)))
+    (transformers modeling_qwen3_5_moe.py:870-875); ``ln_w`` is post_attention_layernorm's
+    [H] bf16 weight (scale 1 + ln_w).  Other arguments and the result as moe_block."""
+    _need(ln_w, "ln_w", torch.bfloat16, (shape.hidden,), h.device)
+    return moe_block(shape, h, table, workspace, _ln=(ln_w, float(eps)), **kw)
+
+
 def moe_block(shape: MoEShape, x, table, workspace: Workspace, router_w=None, logits=None, shared=None,
-              heat=None, out=None, ids=None, weights=None):
+              heat=None, out=None, ids=None, weights=None, _ln=None):
     """Router + routed experts + shared expert + combine; returns (out, ids, weights).
 
     ``shared`` = (gate_proj [Is,H], up_proj [Is,H], down_proj [H,Is], shared_expert_gate [1,H] or [H]).
@@ -225,8 +233,9 @@ def moe_block(shape: MoEShape, x, table, workspace: Workspace, router_w=None, lo
     ids = torch.empty(T, k, dtype=torch.int64, device=dev) if ids is None else ids
     weights = torch.empty(T, k, dtype=torch.bfloat16, device=dev) if weights is None else weights
     buf = workspace.ensure(T)
-    fn = "tmoe_moe_block_int4" if q4 else "tmoe_moe_block_bf16"
-    st = getattr(lib(), fn)(_p(x), T, _p(router_w) if logits is None else None, _p(logits), _p(table),
+    ln = [] if _ln is None else [_p(_ln[0]), _ln[1]]
+    fn = ("tmoe_moe_layer_" if _ln is not None else "tmoe_moe_block_") + ("int4" if q4 else "bf16")
+    st = getattr(lib(), fn)(_p(x), T, *ln, _p(router_w) if logits is None else None, _p(logits), _p(table),
                             *[_p(t) for t in sh], H, E, I, k, Is if shared is not None else 0, _p(out),
                             _p(ids), _p(weights), _p(heat), _p(buf), buf.numel(), _stream(dev))
     check(st, fn)
