@@ -18,6 +18,7 @@ bf16) on a bounded sample as ``cpu_baseline``.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-int4] [--no-stack]
 """
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -191,6 +192,34 @@ def main():
         "hbm_gbps": round(gbs, 1),
         "tokens_per_s_48_layers": round(1e6 / (48 * us), 2),
     }
+
+    # The MoE sublayer (post-attention RMSNorm fused into the input, residual add into the
+    # combine) on the same rotation: what the fused norm and residual cost on top.
+    fnl = lib().tmoe_moe_layer_bf16
+    gen = torch.Generator().manual_seed(7)
+    ln_ws = [(torch.randn(H, generator=gen) * 0.1).to(torch.bfloat16).to(dev) for _ in range(L)]
+    KL = min(K, 1000)
+
+    def layer_args(l, r):
+        a = args_for(l, r)
+        return (a[0], 1, ln_ws[l].data_ptr(), ctypes.c_float(1e-6)) + a[2:]
+
+    lplan = [layer_args(s % L, s // L) for s in range(W + KL)]
+    for a in lplan[:W]:
+        fnl(*a)
+    torch.cuda.synchronize()
+    e0.record()
+    for a in lplan[W:]:
+        if fnl(*a):
+            raise RuntimeError("tmoe_moe_layer_bf16 failed")
+    e1.record()
+    torch.cuda.synchronize()
+    ws.status()
+    us_l = e0.elapsed_time(e1) * 1e3 / KL
+    log(f"layer (RMSNorm + block + residual): {us_l:.2f} us/token-layer")
+    result["layer"] = {"workload": "the MoE sublayer at the same shape, batch 1: bf16(h + block(rmsnorm(h))), the "
+                                   "norm formed in every fused-decode task, the residual added in its combine",
+                       "us_per_token_layer": round(us_l, 3), "over_block_us": round(us_l - us, 3), "steps": KL}
 
     if args.calibrate_copy:
         # Plain device copies of a known size: under `rocprofv3 --pmc FETCH_SIZE` /

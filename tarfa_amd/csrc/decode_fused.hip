@@ -203,13 +203,10 @@ struct RouteLds {
 constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
 
 // SwiGLU of gate/up row pairs [i0, i0 + P): P / 2 tagged activation pairs.
-template <int MH, bool EXACT, int P, typename Take>
+template <int MH, bool EXACT, int P, bool LATE_X, typename XGet, typename Take>
 __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* up, int i0, int n_rows, int K,
-                                         const uint16_t* x, const uint16_t* ln_w, float eps, int lane, uint64_t* act64,
-                                         uint32_t tag, Take&& take) {
+                                         XGet&& get_x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
   static_assert(P % 2 == 0, "activations are published as tagged bf16 pairs");
-  XPack<MH> xf;
-  load_x<MH, EXACT>(xf, x, ln_w, eps, K, lane);
   const uint16_t* rows[2 * P];
 #pragma unroll
   for (int q = 0; q < P; ++q) {
@@ -218,7 +215,13 @@ __device__ __forceinline__ void up_pairs(const uint16_t* gate, const uint16_t* u
     rows[P + q] = up + (size_t)i * K;
   }
   float d[2 * P];
-  wave_dots_p<MH, 2 * P, EXACT>(rows, xf, K, lane, d);
+  if constexpr (LATE_X) {
+    wave_dots_late_x<MH, 2 * P, EXACT>(rows, get_x, K, lane, d);
+  } else {
+    XPack<MH> xf;
+    get_x(xf, lane);
+    wave_dots_p<MH, 2 * P, EXACT>(rows, xf, K, lane, d);
+  }
   int pk[P / 2];
 #pragma unroll
   for (int h = 0; h < P / 2; ++h) {
@@ -263,15 +266,14 @@ __device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act
 // [2I, H/2], scales [2I, H/128]): fp32 gate and up values (no rounding), then
 // act = bf16(silu(g) * u) in fp32 (tarfa/engine/moe_kernel.py:100), published as R/2
 // tagged bf16 pairs.  Loads in need order: input, scales, then the 2R weight rows.
-template <int MH, int R, typename Take>
+template <int MH, int R, typename XGet, typename Take>
 __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int i0, int I, int H,
-                                      const uint16_t* x, const uint16_t* ln_w, float eps, int lane, uint64_t* act64,
-                                      uint32_t tag, Take&& take) {
+                                      XGet&& get_x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
   constexpr int G = 4 * MH;            // scale groups per row (H = 512 MH)
   constexpr int NW = R * G / 2;        // scale words of R rows
   static_assert(R % 2 == 0 && NW <= 128, "scale words of a block fit two per lane");
   XPack<MH> xf;
-  load_x<MH, true>(xf, x, ln_w, eps, H, lane);
+  get_x(xf, lane);
   // Scale words of the R gate rows and of the R up rows: word i of a block in lane i % 64, register i / 64.
   const uint32_t* sg = reinterpret_cast<const uint32_t*>(gs + (size_t)i0 * G);
   const uint32_t* su = reinterpret_cast<const uint32_t*>(gs + (size_t)(I + i0) * G);
@@ -631,22 +633,35 @@ __device__ __forceinline__ int wave_slot_expert(const DecodeParams& p, int j, ui
 }
 
 // Router rows [4t, 4t + 4) of E + 1 (row E: the shared-gate weight).
-template <int MH, bool EXACT, typename Take>
-__device__ __forceinline__ void task_router(const DecodeParams& p, int t, int lane, uint32_t tag, Take&& take) {
+// LATE_X: the input is produced after the rows' loads are issued (a wave's first router
+// task forms the normalised input then, overlapping the rows' latency).
+template <int MH, bool EXACT, bool LATE_X, typename XGet, typename Take>
+__device__ __forceinline__ void task_router(const DecodeParams& p, int t, int lane, XGet&& get_x, uint32_t tag,
+                                            Take&& take) {
   const int n_lrows = p.logits_in ? 0 : p.E;
   const int n_rows = n_lrows + (p.sh_gate ? 1 : 0);
   const int r0 = t * kRouterRows;
   if (r0 >= n_rows) return;
-  XPack<MH> xf;
-  load_x<MH, EXACT>(xf, p.x, p.ln_w, p.ln_eps, p.H, lane);
-  const uint16_t* rp[kRouterRows];
-#pragma unroll
-  for (int r = 0; r < kRouterRows; ++r) {
-    const int row = min(r0 + r, n_rows - 1);
-    rp[r] = row < n_lrows ? p.router_w + (size_t)row * p.H : p.sh_gate_w;
-  }
   float d[kRouterRows];
-  wave_dots_p<MH, kRouterRows, EXACT>(rp, xf, p.H, lane, d);
+  if constexpr (LATE_X) {
+    const uint16_t* rp[kRouterRows];
+#pragma unroll
+    for (int r = 0; r < kRouterRows; ++r) {
+      const int row = min(r0 + r, n_rows - 1);
+      rp[r] = row < n_lrows ? p.router_w + (size_t)row * p.H : p.sh_gate_w;
+    }
+    wave_dots_late_x<MH, kRouterRows, EXACT>(rp, get_x, p.H, lane, d);
+  } else {
+    XPack<MH> xf;
+    get_x(xf, lane);
+    const uint16_t* rp[kRouterRows];
+#pragma unroll
+    for (int r = 0; r < kRouterRows; ++r) {
+      const int row = min(r0 + r, n_rows - 1);
+      rp[r] = row < n_lrows ? p.router_w + (size_t)row * p.H : p.sh_gate_w;
+    }
+    wave_dots_p<MH, kRouterRows, EXACT>(rp, xf, p.H, lane, d);
+  }
   take();
   // One store instruction: lane l writes rows 2 (l % 2) and 2 (l % 2) + 1 of copy l / 2 as
   // one 16-byte store of two tagged words (the task's rows are consecutive logit indices,
@@ -678,6 +693,8 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
   const int r = lane & (kDownRows - 1);
+  // The residual row (layer mode), requested before the wait for the other slots.
+  const float hres = p.resid ? bf16_to_f32(p.resid[h0 + r]) : 0.f;
   // Word j holds this lane's row of slot j (j < k - 1) or, at j = k - 1, of the
   // shared expert (slot k); words past that are never used.
   uint32_t pr[kFusedMaxK];
@@ -724,7 +741,7 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
     for (int j = 1; j < kFusedMaxK; ++j) ps = j == k - 1 ? pr[j] : ps;
     acc = rbf16(acc + rbf16(g * ((r & 1) ? bf16_hi(ps) : bf16_lo(ps))));
   }
-  if (p.resid && lane < kDownRows) acc = bf16_to_f32(p.resid[h0 + lane]) + acc;   // the layer's residual add
+  if (p.resid) acc = hres + acc;   // the layer's residual add
   if (lane < kDownRows) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
@@ -740,6 +757,8 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
   const int r = lane & (RQ - 1);
+  // The residual row (layer mode), requested before the wait for the other slots.
+  const float hres = p.resid ? bf16_to_f32(p.resid[h0 + r]) : 0.f;
   uint32_t pr[kFusedMaxK];   // word j: this lane's row of slot j (j < k - 1) or of the shared expert (j = k - 1)
   Backoff<4> b;
   for (;;) {
@@ -782,7 +801,7 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
     for (int j = 1; j < kFusedMaxK; ++j) ps = j == k - 1 ? pr[j] : ps;
     acc = rbf16(acc + rbf16(g * __uint_as_float(ps)));
   }
-  if (p.resid && lane < RQ) acc = bf16_to_f32(p.resid[h0 + lane]) + acc;   // the layer's residual add
+  if (p.resid) acc = hres + acc;   // the layer's residual add
   if (lane < RQ) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
@@ -901,6 +920,30 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   }
   constexpr bool DYN = dynamic_tickets<Q4>();
   uint32_t* draw = line(p, kLnQueueExit + q) + kQueueDrawWord;
+  // The input fragment: loaded per task; with LN formed once per wave (the norm needs a
+  // wave reduction over h) and kept in registers for the wave's later tasks.
+  XPack<MH> xcache;
+  bool have_x = false;
+  auto get_x = [&](XPack<MH>& xf, int lane) {
+    if constexpr (LN) {
+      if (!have_x) {
+        load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane);
+        have_x = true;
+      }
+      xf = xcache;
+    } else {
+      load_xpack<MH, EXACT>(xf, p.x, p.H, lane);
+    }
+  };
+  // Waves whose first task is not a router task form x at once: most of them next wait for
+  // the routing, which this overlaps (router waves form it inside their task instead,
+  // behind their rows' loads).
+  if constexpr (LN) {
+    if (q + kQueues * (int)rank >= p.n_r) {
+      load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane0);
+      have_x = true;
+    }
+  }
   uint32_t ticket = rank;
   for (uint32_t i = 0;; ++i) {
     const int t = q + kQueues * (int)ticket;
@@ -939,7 +982,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       if (t == p.n_r) publish_routing(p, lane, rwc);   // task n_r: the first gate/up task of slot 0
     }
     if (tk.type == kTR) {
-      task_router<MH, EXACT>(p, tk.idx, lane, tag, take);
+      task_router<MH, EXACT, LN>(p, tk.idx, lane, get_x, tag, take);
     } else if (tk.type == kTS || tk.type == kTG) {
       // Gate/up pairs: the shared expert (S) or routed slot j (G); one call site.
       const bool shared = tk.type == kTS;
@@ -949,13 +992,13 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         if (e >= 0)
           up_q4<MH, kQ4Pairs>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 1)), tk.idx * kQ4Pairs, p.I, p.H,
-                    p.x, p.ln_w, p.ln_eps, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag, take);
+                    get_x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag, take);
       } else if (e >= 0) {
         const uint16_t* gu = shared ? nullptr : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e));
         const uint16_t* g = shared ? p.sh_gate : gu;
         const uint16_t* u = shared ? p.sh_up : gu + (size_t)p.I * p.H;
         constexpr int P = Q4 ? kQ4SPairs : kPairs;
-        up_pairs<MH, EXACT, P>(g, u, tk.idx * P, n_rows, p.H, p.x, p.ln_w, p.ln_eps, lane,
+        up_pairs<MH, EXACT, P, LN && !Q4>(g, u, tk.idx * P, n_rows, p.H, get_x, lane,
                             p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag, take);
       }
     } else if (Q4 && tk.type == kTD) {

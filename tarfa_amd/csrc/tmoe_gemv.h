@@ -142,6 +142,30 @@ __device__ __forceinline__ void wave_dots_p(const uint16_t* const (&rows)[R], co
   }
 }
 
+// As wave_dots_p, with the fragment produced after the weight loads are issued (get_x
+// may compute it: its latency then overlaps theirs).
+template <int MAXC, int R, bool EXACT, typename XGet>
+__device__ __forceinline__ void wave_dots_late_x(const uint16_t* const (&rows)[R], XGet&& get_x, int K, int lane,
+                                                 float (&out)[R]) {
+  u32x4 w[R][MAXC];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int col = c * 512 + lane * 8;
+      w[r][c] = (EXACT || col < K) ? ld_stream(rows[r] + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+  XPack<MAXC> xf;
+  get_x(xf, lane);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) acc = dot8p(w[r][c], xf.v[c], acc);
+    out[r] = wave_sum(acc);
+  }
+}
+
 // Top-k of E fp32 logits by one wave (lane l owns experts l + 64 i, i < MAXEPL).
 // Order: logit descending, ties to the lower expert index.  Probabilities are
 // softmax in fp32 (max-subtracted), renormalised over the k selected in router
