@@ -69,3 +69,15 @@ def test_entry_points_reject_bad_arguments_without_touching_the_device():
     assert lib.tmoe_quantize_int4(p, 4, 256, 3, p, p, None) == -2                     # odd G
     assert lib.tmoe_dequant_int4_bf16(p, p, 4, 260, 130, p, None) == -2               # K % 8
     assert lib.tmoe_dequant_int4_bf16(p + 2, p, 4, 256, 128, p, None) == -3           # packed alignment
+    # the MoE sublayer entry points: the norm weight is required, out must not alias h, eps >= 0
+    for fn in (lib.tmoe_moe_layer_bf16, lib.tmoe_moe_layer_int4):
+        assert fn(p, 1, None, 1e-6, p, None, p, None, None, None, None, 2560, 256, 1024, 8, 0,
+                  512, None, None, None, p, 1 << 30, None) == -1
+        assert fn(p, 1, p, 1e-6, p, None, p, None, None, None, None, 2560, 256, 1024, 8, 0,
+                  p, None, None, None, p, 1 << 30, None) == -2                          # out == h
+        assert fn(p, 1, p, -1.0, p, None, p, None, None, None, None, 2560, 256, 1024, 8, 0,
+                  512, None, None, None, p, 1 << 30, None) == -2                        # eps < 0
+        assert fn(p, 1, p + 2, 1e-6, p, None, p, None, None, None, None, 2560, 256, 1024, 8, 0,
+                  512, None, None, None, p, 1 << 30, None) == -3                        # ln_w alignment
+    # T * k above 524288 (the dispatch's LDS mask)
+    assert lib.tmoe_dispatch(p, 65537, 8, 16, p, p, p, p, 1 << 40, None) == -2
