@@ -868,7 +868,9 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 // accumulator); this kernel applies the routing weight and the shared gate, each product
 // rounded to bf16, then accumulates in the reference's order (the token's experts
 // ascending, ties in slot order, then the shared expert), rounding to bf16 after every
-// addition.  Lanes 0..k-1 read the token's k entries at once and rank them.
+// addition.  Lanes 0..k-1 read the token's k entries at once and rank them.  NSPLIT waves
+// share a token, wave j taking chunks j MAXC .. j MAXC + MAXC - 1 (few tokens: one chunk per
+// wave).
 template <int MAXC, int MAXK>
 __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int64_t* ids64,
                                                  const int32_t* __restrict__ inv, const uint16_t* __restrict__ ch,
@@ -877,7 +879,9 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
                                                  const uint16_t* __restrict__ resid, int T, int H, int E, int k,
                                                  uint16_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nsplit = (((H + 511) / 512) + MAXC - 1) / MAXC;
+  const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = wv / nsplit, cbase = (wv - t * nsplit) * MAXC * 512;
   if (t >= T) return;
   int e = 0x7FFFFFFF, r = 0;
   float w = 0.f;
@@ -921,7 +925,7 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
   const float gv = sh ? gs[t] : 0.f;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
-    const int col = c * 512 + lane * 8;
+    const int col = cbase + c * 512 + lane * 8;
     if (col >= H) continue;
     u32x4 v[MAXK];
 #pragma unroll
@@ -1032,13 +1036,17 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   }
 
   const int nc = (H + 511) / 512;
-  const dim3 gc((T + 3) / 4), bc(256);
+  const bool split = T < 512;        // few tokens: one wave per (token, 512-column chunk)
+  const dim3 gc(((size_t)T * (split ? nc : 1) + 3) / 4), bc(256);
   const uint16_t* shp = has_sh ? sh : nullptr;
   auto combine = [&](auto kern) {
     hipLaunchKernelGGL(kern, gc, bc, 0, s, ids32, ids64, inv, ch, wf, wb, shp, gs, resid, T, H, E, k, out);
   };
-  const int mc = nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8;
-  if (k <= 8) {
+  const int mc = split ? 1 : nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8;
+  if (mc == 1) {
+    if (k <= 8) combine(k_combine<1, 8>);
+    else combine(k_combine<1, 16>);
+  } else if (k <= 8) {
     if (mc == 2) combine(k_combine<2, 8>);
     else if (mc == 4) combine(k_combine<4, 8>);
     else if (mc == 6) combine(k_combine<6, 8>);

@@ -7,8 +7,9 @@
 
 namespace tmoe {
 
-// logits[t, e] = sum_h x[t, h] * wg[e, h] in fp32.  One block per token; wave w
-// handles experts w, w + 4, ...  (4 rows in flight per wave).
+// logits[t, e] = sum_h x[t, h] * wg[e, h] in fp32.  Block (t, y) of a (T, Y) grid: wave w
+// handles experts 16 y + 4 w .. + 3, then 16 (y + Y) + 4 w, ... (4 rows in flight per
+// wave).  Few tokens take Y = E / 16 (one round trip per wave), many take Y = 1.
 template <int MAXC>
 __global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restrict__ x,
                                                        const uint16_t* __restrict__ wg, int H, int E,
@@ -17,7 +18,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restric
   const int t = blockIdx.x;
   XFrag<MAXC> xf;
   load_xfrag<MAXC>(xf, x + (size_t)t * H, H, lane);
-  for (int e0 = wid * 4; e0 < E; e0 += 16) {
+  for (int e0 = (int)blockIdx.y * 16 + wid * 4; e0 < E; e0 += 16 * (int)gridDim.y) {
     const uint16_t* rows[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) rows[r] = wg + (size_t)min(e0 + r, E - 1) * H;
@@ -51,11 +52,12 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
 int launch_router_logits(const uint16_t* x, const uint16_t* wg, int T, int H, int E, float* logits,
                          hipStream_t s) {
   const int nc = (H + 511) / 512;
+  const dim3 g(T, T < 512 ? (E + 15) / 16 : 1);
   switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
-    case 2: hipLaunchKernelGGL(k_router_logits<2>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
-    case 4: hipLaunchKernelGGL(k_router_logits<4>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
-    case 6: hipLaunchKernelGGL(k_router_logits<6>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
-    default: hipLaunchKernelGGL(k_router_logits<8>, dim3(T), dim3(256), 0, s, x, wg, H, E, logits); break;
+    case 2: hipLaunchKernelGGL(k_router_logits<2>, g, dim3(256), 0, s, x, wg, H, E, logits); break;
+    case 4: hipLaunchKernelGGL(k_router_logits<4>, g, dim3(256), 0, s, x, wg, H, E, logits); break;
+    case 6: hipLaunchKernelGGL(k_router_logits<6>, g, dim3(256), 0, s, x, wg, H, E, logits); break;
+    default: hipLaunchKernelGGL(k_router_logits<8>, g, dim3(256), 0, s, x, wg, H, E, logits); break;
   }
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
