@@ -66,48 +66,102 @@ def profiled_traffic(name, key="traffic_bytes_per_launch"):
     return None
 
 
-def cpu_threads():
-    try:
-        n = len(os.sched_getaffinity(0))
-    except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))          # this GPU's share of the host
-
-
-def cpu_model():
+def host_cpu():
+    """(model name, physical cores, logical CPUs of the host, CPUs this process may use)."""
+    model, cores = "unknown", set()
+    phys = core = None
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
     except OSError:
         pass
-    return "unknown"
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return model, len(cores) or None, os.cpu_count() or 1, usable
 
 
-def main():
+def leg_steps(args):
+    """Timed steps of every decode leg: the headline (bf16 block), the sublayer and int4."""
+    K = args.steps
+    return {"decode": K,
+            "layer": K if args.layer_steps is None else args.layer_steps,
+            "int4": K if args.int4_steps is None else args.int4_steps}
+
+
+def token_rows(L, warmup, steps):
+    """Per-layer token rows every decode leg needs: step s of a leg runs layer s % L on that
+    layer's token row s // L, for s < warmup + steps."""
+    return (warmup + max(steps.values()) + L - 1) // L
+
+
+def step_plan(L, warmup, steps):
+    """(layer, row) of each of the warmup + steps launches of one leg."""
+    return [(s % L, s // L) for s in range(warmup + steps)]
+
+
+def cpu_threads(usable):
+    return max(1, min(16, usable))     # this GPU's share of the host
+
+
+def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--layers", type=int, default=48,
                     help="resident seeded layers (48 = the whole stack, 194 GB of bf16 experts)")
+    ap.add_argument("--layer-steps", type=int, default=None, help="timed steps of the sublayer leg (default --steps)")
+    ap.add_argument("--int4-steps", type=int, default=None, help="timed steps of the int4 leg (default --steps)")
     ap.add_argument("--stack-tokens", type=int, default=64)
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=6)
-    ap.add_argument("--cpu-tokens", type=int, default=4096,
-                    help="decode tokens of the CPU baseline sample (~8 s of host work at the default)")
+    ap.add_argument("--cpu-tokens", type=int, default=200,
+                    help="decode tokens of each CPU baseline decode sample (median reported)")
+    ap.add_argument("--cpu-prefill-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-int4", action="store_true")
-    ap.add_argument("--int4-steps", type=int, default=2000)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain device copies of known size (scale for HBM byte counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the MoE layer is not sharded across "
-              "GPUs in this build.", file=sys.stderr)
-        return 2
+    return ap.parse_args(argv)
 
+
+class _Timer:
+    """HIP events on the launch stream (torch's current stream, which every leg launches on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.e0 = torch.cuda.Event(enable_timing=True)
+        self.e1 = torch.cuda.Event(enable_timing=True)
+
+    def run(self, fn, plan, warmup):
+        for a in plan[:warmup]:
+            fn(a)
+        self.torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self.e0.record()
+        for a in plan[warmup:]:
+            fn(a)
+        self.e1.record()
+        self.torch.cuda.synchronize()
+        return self.e0.elapsed_time(self.e1), time.perf_counter() - t0
+
+
+def run(args, log):
     import torch
     from tarfa_amd import seeded
     from tarfa_amd import moe as tm
@@ -118,57 +172,48 @@ def main():
 
     dev = torch.device("cuda:0")
     shape = MoEShape(2560, 256, 1024, 8, 1024)
-    L, K, W = args.layers, args.steps, args.warmup
+    L, W = args.layers, args.warmup
+    steps = leg_steps(args)
+    K = steps["decode"]
     H = shape.hidden
-    log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+    timer = _Timer(torch)
 
     # ---------------- setup: the L seeded full-size layers resident in HBM (residency ledger),
-    # per-layer router / shared-expert weights and token streams
+    # per-layer router / shared-expert weights and token rows for every decode leg
     t0 = time.perf_counter()
     ledger = ResidencyLedger(shape, L, dev)
     ledger.fill_seeded(1)
-
-    class _Layer:
-        def __init__(self, l):
-            self.router_w, self.shared = seeded.make_block_weights(shape, 1, l, dev)
-
-    layers = [_Layer(l) for l in range(L)]
+    layers = [LayerWeights(*seeded.make_block_weights(shape, 1, l, dev)) for l in range(L)]
     tables = [ledger.tables[l] for l in range(L)]
-    per_layer = (K + W + L - 1) // L + 1
-    xs = [seeded.make_tokens(shape, 1, per_layer, layer=l, device=dev) for l in range(L)]
+    rows = token_rows(L, W, steps)
+    xs = [seeded.make_tokens(shape, 1, rows, layer=l, device=dev) for l in range(L)]
     ws = Workspace(shape, dev)
     out = torch.empty(1, H, dtype=torch.bfloat16, device=dev)
     ids = torch.empty(1, shape.top_k, dtype=torch.int64, device=dev)
     wts = torch.empty(1, shape.top_k, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
-    log(f"setup {time.perf_counter() - t0:.1f}s: {L} resident layers x {prefill_weight_bytes(shape) / 1e9:.2f} GB")
+    log(f"setup {time.perf_counter() - t0:.1f}s: {L} resident layers x {prefill_weight_bytes(shape) / 1e9:.2f} GB, "
+        f"{rows} token rows per layer")
 
     # Lean launch path: prebuilt ctypes arguments, one C call per step.
-    fn = lib().tmoe_moe_block_bf16
     stream = torch.cuda.current_stream(dev).cuda_stream
     wsp, wsn = ws.buf.data_ptr(), ws.buf.numel()
 
-    def args_for(l, r):
+    def block_args(l, r, table=None):
         ly = layers[l]
         sh = [t.data_ptr() for t in ly.shared]
-        return (xs[l][r].data_ptr(), 1, ly.router_w.data_ptr(), None, tables[l].data_ptr(), *sh, H,
+        return (xs[l][r].data_ptr(), 1, ly.router_w.data_ptr(), None, (tables[l] if table is None else table).data_ptr(), *sh, H,
                 shape.num_experts, shape.intermediate, shape.top_k, shape.shared_intermediate, out.data_ptr(),
                 ids.data_ptr(), wts.data_ptr(), None, wsp, wsn, stream)
 
-    plan = [args_for(s % L, s // L) for s in range(W + K)]
-    for a in plan[:W]:
-        fn(*a)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for a in plan[W:]:
-        if fn(*a):
-            raise RuntimeError("tmoe_moe_block_bf16 failed")
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_time(e1)
+    def launcher(fn, name):
+        def go(a):
+            if fn(*a):
+                raise RuntimeError(f"{name} failed")
+        return go
+
+    plan = [block_args(l, r) for l, r in step_plan(L, W, K)]
+    gpu_ms, wall = timer.run(launcher(lib().tmoe_moe_block_bf16, "tmoe_moe_block_bf16"), plan, W)
     ws.status()
     us = gpu_ms * 1e3 / K
     nbytes = decode_bytes(shape)
@@ -195,30 +240,21 @@ def main():
 
     # The MoE sublayer (post-attention RMSNorm fused into the input, residual add into the
     # combine) on the same rotation: what the fused norm and residual cost on top.
-    fnl = lib().tmoe_moe_layer_bf16
     gen = torch.Generator().manual_seed(7)
     ln_ws = [(torch.randn(H, generator=gen) * 0.1).to(torch.bfloat16).to(dev) for _ in range(L)]
-    KL = min(K, 1000)
+    KL = steps["layer"]
 
     def layer_args(l, r):
-        a = args_for(l, r)
+        a = block_args(l, r)
         return (a[0], 1, ln_ws[l].data_ptr(), ctypes.c_float(1e-6)) + a[2:]
 
-    lplan = [layer_args(s % L, s // L) for s in range(W + KL)]
-    for a in lplan[:W]:
-        fnl(*a)
-    torch.cuda.synchronize()
-    e0.record()
-    for a in lplan[W:]:
-        if fnl(*a):
-            raise RuntimeError("tmoe_moe_layer_bf16 failed")
-    e1.record()
-    torch.cuda.synchronize()
+    lplan = [layer_args(l, r) for l, r in step_plan(L, W, KL)]
+    gpu_ms, _ = timer.run(launcher(lib().tmoe_moe_layer_bf16, "tmoe_moe_layer_bf16"), lplan, W)
     ws.status()
-    us_l = e0.elapsed_time(e1) * 1e3 / KL
+    us_l = gpu_ms * 1e3 / KL
     log(f"layer (RMSNorm + block + residual): {us_l:.2f} us/token-layer")
     result["layer"] = {"workload": "the MoE sublayer at the same shape, batch 1: bf16(h + block(rmsnorm(h))), the "
-                                   "norm formed in every fused-decode task, the residual added in its combine",
+                                   "norm formed once per fused-decode wave, the residual added in its combine",
                        "us_per_token_layer": round(us_l, 3), "over_block_us": round(us_l - us, 3), "steps": KL}
 
     if args.calibrate_copy:
@@ -236,28 +272,12 @@ def main():
     if not args.no_int4:
         t0 = time.perf_counter()
         q4 = ResidencyLedger.quantized_from(ledger)
-        q4_tables = [q4.tables[l] for l in range(L)]
         log(f"int4 setup {time.perf_counter() - t0:.1f}s")
-        fn4 = lib().tmoe_moe_block_int4
-        K4 = args.int4_steps
-
-        def args_q4(l, r):
-            a = list(args_for(l, r))
-            a[4] = q4_tables[l].data_ptr()
-            return tuple(a)
-
-        plan4 = [args_q4(s % L, s // L) for s in range(W + K4)]
-        for a in plan4[:W]:
-            fn4(*a)
-        torch.cuda.synchronize()
-        e0.record()
-        for a in plan4[W:]:
-            if fn4(*a):
-                raise RuntimeError("tmoe_moe_block_int4 failed")
-        e1.record()
-        torch.cuda.synchronize()
+        K4 = steps["int4"]
+        plan4 = [block_args(l, r, q4.tables[l]) for l, r in step_plan(L, W, K4)]
+        gpu_ms, _ = timer.run(launcher(lib().tmoe_moe_block_int4, "tmoe_moe_block_int4"), plan4, W)
         ws.status()
-        us4 = e0.elapsed_time(e1) * 1e3 / K4
+        us4 = gpu_ms * 1e3 / K4
         nb4 = decode_bytes_int4(shape)
         gbs4 = nb4 / (us4 * 1e-6) / 1e9
         result["int4"] = {"workload": "labelled int4 fast mode at the same layer shape, batch 1: routed experts "
@@ -280,18 +300,12 @@ def main():
 
             def prefill4(i):
                 l = i % len(plg4)
-                tm.moe_block(shape, px4, q4_tables[l], pws4, logits=plg4[l], shared=layers[l].shared, out=pout4,
+                tm.moe_block(shape, px4, q4.tables[l], pws4, logits=plg4[l], shared=layers[l].shared, out=pout4,
                              ids=pi4, weights=pw4)
 
-            prefill4(0)
-            torch.cuda.synchronize()
-            e0.record()
-            for i in range(1, P4 + 1):
-                prefill4(i)
-            e1.record()
-            torch.cuda.synchronize()
+            gpu_ms, _ = timer.run(prefill4, list(range(P4 + 1)), 1)
             pws4.status()
-            pus4 = e0.elapsed_time(e1) * 1e3 / P4
+            pus4 = gpu_ms * 1e3 / P4
             # routed: 3*H*I nibbles + one bf16 scale per 128 columns per expert; shared expert bf16
             wb4 = shape.num_experts * 3 * H * shape.intermediate * (64 + 2) // 128 + \
                 2 * 3 * H * shape.shared_intermediate
@@ -304,7 +318,7 @@ def main():
                                                             "int4_traffic_bytes_per_launch")}
             log(f"int4 prefill: {pus4:.1f} us/layer")
             del pws4, px4, plg4
-        del q4, q4_tables, plan4
+        del q4, plan4
 
     # ---------------- prefill: T = 4096 through the same layer shape, logits supplied
     if not args.no_prefill:
@@ -323,15 +337,9 @@ def main():
             tm.moe_block(shape, px[l], tables[l], pws, logits=plg[l],
                          shared=layers[l].shared, out=pout, ids=pids, weights=pw)
 
-        prefill(0)
-        torch.cuda.synchronize()
-        e0.record()
-        for i in range(1, P + 1):
-            prefill(i)
-        e1.record()
-        torch.cuda.synchronize()
+        gpu_ms, _ = timer.run(prefill, list(range(P + 1)), 1)
         pws.status()
-        pus = e0.elapsed_time(e1) * 1e3 / P
+        pus = gpu_ms * 1e3 / P
         fl = prefill_flops(shape, T)
         wb = prefill_weight_bytes(shape)
         tflops = fl / (pus * 1e-6) / 1e12
@@ -346,27 +354,19 @@ def main():
                              "flops": fl, "weight_bytes": wb, "tokens_per_s": round(T / (pus * 1e-6), 1),
                              "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_p_prefill_t4096_h2560_e256_i1024_k8.md")}
         log(f"prefill: {pus:.1f} us/layer, {tflops:.1f} TFLOP/s, weights {wgbs:.0f} GB/s")
-        del pws
+        del pws, px, plg
 
     # ---------------- the whole stack: 48 resident layers, batch-1 decode of consecutive tokens,
     # per-layer router logits with Zipf(1.1) expert popularity (heat ledger + route telemetry on)
     if not args.no_stack:
         NT, NW = args.stack_tokens, 4
-        blocks = [LayerWeights(ly.router_w, ly.shared) for ly in layers]
-        stack = MoEStack(ledger, blocks)
+        stack = MoEStack(ledger, layers)
         ledger.heat.zero_()
         slg, _ = zipf_logits(shape, L, NT + NW, seed=11, device=dev)
         sx = seeded.make_tokens(shape, 3, NT + NW, device=dev)
-        for t in range(NW):
-            stack.decode(sx[t:t + 1], slg[t])
-        torch.cuda.synchronize()
-        e0.record()
-        for t in range(NW, NW + NT):
-            stack.decode(sx[t:t + 1], slg[t])
-        e1.record()
-        torch.cuda.synchronize()
+        gpu_ms, _ = timer.run(lambda t: stack.decode(sx[t:t + 1], slg[t]), list(range(NW + NT)), NW)
         stack.status()
-        ms_tok = e0.elapsed_time(e1) / NT
+        ms_tok = gpu_ms / NT
         # logits are supplied: per layer the routed experts, the shared expert and the shared gate row are read
         tok_bytes = L * (decode_bytes(shape) - 2 * shape.num_experts * H)
         heat = ledger.heat.cpu()
@@ -385,32 +385,88 @@ def main():
 
     # ---------------- CPU baseline: the reference's op chain in torch bf16 on the host
     if not args.no_cpu:
-        from oracle import cpu_reference as cref
-        nt = cpu_threads()
-        torch.set_num_threads(nt)
-        ly = layers[0]
-        gu, dn = ledger.hbm[0][0].cpu(), ledger.hbm[0][1].cpu()
-        wg = ly.router_w.cpu()
-        shw = tuple(t.cpu() for t in ly.shared)
-        xc = seeded.make_tokens(shape, 4, args.cpu_tokens, device=dev).cpu()
-        for r in range(2):
-            cref.moe_block(xc[r:r + 1], wg, shape.top_k, gu, dn, shape.num_experts, shw)
-        times = []
-        t_all = time.perf_counter()
-        for r in range(args.cpu_tokens):
-            t1 = time.perf_counter()
-            cref.moe_block(xc[r:r + 1], wg, shape.top_k, gu, dn, shape.num_experts, shw)
-            times.append(time.perf_counter() - t1)
-        cpu_us = statistics.median(times) * 1e6
-        result["cpu_baseline"] = {
-            "value": round(cpu_us, 1), "unit": "us/token-layer", "cores": nt, "kind": "port",
-            "sample": f"median of {args.cpu_tokens} decode tokens through layer 0 (same shape, same seeded "
-                      f"weights), torch {torch.__version__} CPU bf16 op sequence of fused_int4.py:192-194 + "
-                      f"router + shared expert; {cpu_model()}",
-            "gbps": round(nbytes / (cpu_us * 1e-6) / 1e9, 2),
-            "seconds": round(time.perf_counter() - t_all, 1)}
-        log(f"cpu: {cpu_us:.0f} us/token-layer on {nt} threads")
+        result["cpu_baseline"] = cpu_baseline(args, torch, seeded, shape, ledger, layers, nbytes, dev, log)
 
+    torch.cuda.synchronize()
+    return result
+
+
+def cpu_baseline(args, torch, seeded, shape, ledger, layers, nbytes, dev, log):
+    """The reference's op chain (torch CPU bf16) on this host, on bounded samples: decode of the
+    full-size layer (the headline's unit), decode of the small CPU layer (H=1024, E=32, I=512, no
+    shared expert) and one T=4096 prefill chunk through the full-size layer."""
+    from oracle import cpu_reference as cref
+    from tarfa_amd.moe import MoEShape
+
+    model, phys, logical, usable = host_cpu()
+    nt = cpu_threads(usable)
+    torch.set_num_threads(nt)
+    H = shape.hidden
+
+    def median_us(fn, reps, warm=2):
+        for _ in range(warm):
+            fn()
+        times = []
+        for _ in range(reps):
+            t1 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t1)
+        return statistics.median(times) * 1e6
+
+    t_all = time.perf_counter()
+    # full-size layer 0, same seeded weights as the GPU legs
+    gu, dn = ledger.hbm[0][0].cpu(), ledger.hbm[0][1].cpu()
+    wg = layers[0].router_w.cpu()
+    shw = tuple(t.cpu() for t in layers[0].shared)
+    nd = args.cpu_tokens
+    xc = seeded.make_tokens(shape, 4, nd + 2, device=dev).cpu()
+    it = iter(range(nd + 2))
+    us1 = median_us(lambda: cref.moe_block(xc[next(it)][None], wg, shape.top_k, gu, dn, shape.num_experts, shw), nd)
+    # the small CPU layer
+    s0 = MoEShape(1024, 32, 512, 8, 0)
+    l0 = seeded.make_layer(s0, seed=5, device=dev)
+    gu0, dn0, wg0 = l0.gate_up.cpu(), l0.down.cpu(), l0.router_w.cpu()
+    x0 = seeded.make_tokens(s0, 5, nd + 2, device=dev).cpu()
+    it0 = iter(range(nd + 2))
+    us0 = median_us(lambda: cref.moe_block(x0[next(it0)][None], wg0, s0.top_k, gu0, dn0, s0.num_experts), nd)
+    # T = 4096 prefill chunk, logits supplied ~N(0,1), shared expert included
+    T = 4096
+    px = seeded.make_tokens(shape, 2, T, device=dev).cpu()
+    plg = seeded.make_logits(shape, 2, T, device=dev).cpu()
+    sp = median_us(lambda: cref.moe_block(px, wg, shape.top_k, gu, dn, shape.num_experts, shw, logits=plg),
+                   args.cpu_prefill_reps) * 1e-6
+    fl = prefill_flops(shape, T)
+    log(f"cpu: {us1:.0f} us/token-layer (full size), {us0:.0f} us (small layer), prefill {sp:.2f} s/layer "
+        f"on {nt} threads")
+    return {
+        "value": round(us1, 1), "unit": "us/token-layer", "cores": nt, "kind": "port",
+        "sample": f"median of {nd} decode tokens through one full-size layer (same seeded weights as the GPU legs), "
+                  f"torch {torch.__version__} CPU bf16 op sequence of fused_int4.py:192-194 + router + shared "
+                  f"expert; also the small CPU layer (median of {nd}) and one T=4096 prefill chunk "
+                  f"(fused_int4.py:239-244, median of {args.cpu_prefill_reps}); each after 2 warm-up runs",
+        "gbps": round(nbytes / (us1 * 1e-6) / 1e9, 2),
+        "cpu_model": model, "host_physical_cores": phys, "host_logical_cpus": logical,
+        "usable_cpus": usable, "threads": nt,
+        "decode_small_layer_us": round(us0, 1),
+        "prefill_t4096_s_per_layer": round(sp, 3), "prefill_t4096_tflops": round(fl / sp / 1e12, 3),
+        "seconds": round(time.perf_counter() - t_all, 1)}
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the MoE layer is not sharded across "
+              "GPUs in this build.", file=sys.stderr)
+        return 2
+    log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+    result = run(args, log)
+    # Every device object of the run is released by now; drain the device and return the
+    # cached blocks before the interpreter's exit handlers run.
+    import gc
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
 

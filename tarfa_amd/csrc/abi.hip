@@ -40,10 +40,11 @@ static int decode(DecodeParams& p, bool run_router, hipStream_t s) {
 static bool misaligned(const void* p) { return ((uintptr_t)p & 15u) != 0; }
 
 static int check_shape(int T, int H, int E, int I, int k, int Is) {
-  if (T < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E) return TMOE_ERR_SHAPE;
-  if (H < 8 || H > 4096 || H % 8) return TMOE_ERR_SHAPE;
-  if (I < 8 || I > 4096 || I % 8) return TMOE_ERR_SHAPE;
-  if (Is < 0 || Is > 4096 || Is % 8) return TMOE_ERR_SHAPE;
+  // The bounds are the ones the fixed-size decode hand-off area is sized for.
+  if (T < 1 || E < 1 || E > kMaxExperts || k < 1 || k > kMaxTopK || k > E) return TMOE_ERR_SHAPE;
+  if (H < 8 || H > kMaxDim || H % 8) return TMOE_ERR_SHAPE;
+  if (I < 8 || I > kMaxDim || I % 8) return TMOE_ERR_SHAPE;
+  if (Is < 0 || Is > kMaxDim || Is % 8) return TMOE_ERR_SHAPE;
   return TMOE_OK;
 }
 
@@ -80,7 +81,7 @@ extern "C" int tmoe_workspace_status(void* workspace, void* stream) {
   return (flags & kErrTimeout) ? TMOE_ERR_TIMEOUT : TMOE_ERR_EXPERT_ID;
 }
 
-static void bind_ws(DecodeParams& p, void* ws, size_t ws_bytes, const Ws& L) {
+static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
   p.status = ws_ptr<uint32_t>(ws, L.status);
   p.logits_ws = ws_ptr<float>(ws, L.logits);
   p.ids_ws = ws_ptr<int32_t>(ws, L.ids);
@@ -94,8 +95,8 @@ static void bind_ws(DecodeParams& p, void* ws, size_t ws_bytes, const Ws& L) {
   p.lg_stride = logit_stride(p.E);
   p.act64 = p.lg64 + (size_t)kLogitReplicas * p.lg_stride;
   p.dq64 = p.act64 + ((size_t)p.k * p.I + p.Is) / 2;
-  p.handoff = ws_ptr<void>(ws, L.logits);
-  p.handoff_words = (ws_bytes - L.logits) / 8;
+  p.handoff = ws_ptr<void>(ws, L.tagged);
+  p.handoff_words = kHandoffWords;
 }
 
 
@@ -119,7 +120,7 @@ static int experts_forward(const void* x, int T, const int64_t* ids, const void*
     p.w_in = (const uint16_t*)weights;
     p.H = H; p.E = E; p.I = I; p.k = k; p.Is = 0;
     p.out = (uint16_t*)out;
-    bind_ws(p, workspace, ws_bytes, L);
+    bind_ws(p, workspace, L);
     return q4 ? decode_fused_launch(p, false, s) : decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
@@ -176,7 +177,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     p.ids_out = ids_out;
     p.w_out = (uint16_t*)weights_out;
     p.heat = heat;
-    bind_ws(p, workspace, ws_bytes, L);
+    bind_ws(p, workspace, L);
     if (!ln_w) return q4 ? decode_fused_launch(p, true, s) : decode(p, true, s);
     // The fused kernel forms the normalised input in every task and adds the residual in
     // its combine; other shapes normalise first and add the residual after.

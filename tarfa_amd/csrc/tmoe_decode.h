@@ -43,7 +43,7 @@ struct DecodeParams {
   uint64_t* act64;            // [k * I / 2] tagged bf16 activation pairs, then [Is / 2] shared
   uint64_t* dq64;             // [(k + 1) * H] tagged per-slot down results (slot k: shared, before its gate):
                               // bf16 row pairs, or one fp32 row per word in int4 mode
-  void* handoff;              // workspace past the sync lines: zeroed when the epoch wraps
+  void* handoff;              // the fixed-size tagged hand-off area: zeroed when the epoch wraps
   size_t handoff_words;       // its size in uint64
   int n_r, n_s, n_g, n_d, n_sd, n_tasks;   // task counts: router, shared up, gate/up per slot, down per slot,
                                            // shared down; total

@@ -43,9 +43,20 @@ enum RouteWord { kRwId = 0, kRwW = 8, kRwGate = 16, kRouteWords = 17 };
 // 256-byte lines.
 inline int logit_stride(int E) { return ((E + 1) + 31) & ~31; }
 
+// The fused decode's tagged hand-off words live in one area of fixed size, right after the
+// sync lines, sized for the largest shape any entry point accepts (E <= 1024, k <= 16,
+// H, I, Is <= 4096).  Its offset depends on nothing, so no region that a T > 1 call (or
+// tmoe_dispatch, which lays out with placeholder H and I) writes can overlap it: every word
+// in it is zero or was written by a decode call of this workspace, under that call's tag.
+constexpr int kMaxExperts = 1024, kMaxTopK = 16, kMaxDim = 4096;
+constexpr size_t kHandoffWords = (size_t)kLogitReplicas * (((kMaxExperts + 1) + 31) & ~31) +
+                                 ((size_t)kMaxTopK * kMaxDim + kMaxDim) / 2 + (size_t)(kMaxTopK + 1) * kMaxDim;
+
 struct Ws {
   size_t status;   // uint32[kStatusSlots]
   size_t sync;     // uint32[kSyncLines * kLine]   fused decode task-graph lines
+  size_t tagged;   // u64[kHandoffWords]   tagged logit copies [kLogitReplicas * logit_stride(E)], activation
+                   // pairs [(k * I + Is) / 2], per-slot down results [(k + 1) * H] (slot k = shared expert)
   size_t logits;   // f32[T * (E + 1)]   router logits; column E = shared-gate logit (decode)
   size_t ids;      // int32[T * k]
   size_t wts;      // f32[T * k]         routing weights (bf16 values)
@@ -59,8 +70,6 @@ struct Ws {
   size_t ch;       // bf16[T * k * H]    per-assignment expert outputs, unscaled (T > 1)
   size_t desc;     // int32x4[T * k / 64 + E + T / 64 + 2]   prefill M-chunk descriptors (T > 1)
   size_t xn;       // bf16[T * H]        RMSNorm of the hidden state (the layer entry points)
-  size_t tagged;   // u64[kLogitReplicas * logit_stride(E) + (k * I + Is) / 2 + (k + 1) * H]  tagged
-                   // logit copies, activation pairs, per-slot down results (slot k = shared expert)
   size_t total;
 };
 
@@ -74,6 +83,7 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   w.status = take(sizeof(uint32_t) * kStatusSlots);
   w.sync = take(sizeof(uint32_t) * kSyncLines * kLine);
+  w.tagged = take(8 * kHandoffWords);
   w.logits = take(sizeof(float) * t * (size_t)(E + 1));
   w.ids = take(sizeof(int32_t) * t * (size_t)k);
   w.wts = take(sizeof(float) * t * (size_t)k);
@@ -87,8 +97,6 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
   w.desc = take(t > 1 ? 16 * (t * (size_t)k / 64 + (size_t)E + t / 64 + 2) : 0);
   w.xn = take(2 * t * (size_t)H);
-  w.tagged = take(8 * ((size_t)kLogitReplicas * logit_stride(E) + ((size_t)k * I + (size_t)Is) / 2 +
-                        (size_t)(k + 1) * H));
   w.total = o;
   return w;
 }

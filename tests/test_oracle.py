@@ -350,6 +350,77 @@ def test_int4_ffn_group_form_equals_rowscale_form_when_scales_repeat():
     assert rel_l2(a, b) < 1e-6
 
 
+def _distinct_group_scales(g, shape):
+    """bf16 scale bits whose groups within a row all differ: each group of a row takes its own
+    binade (a per-row permutation of 2^-10 .. 2^(ng - 11)) with a random mantissa."""
+    ng = shape[-1]
+    rows = int(np.prod(shape[:-1]))
+    exps = np.stack([g.permutation(ng) for _ in range(rows)]).reshape(shape) - 10
+    s = bf16.bits((2.0 ** exps * g.uniform(1.0, 2.0, shape)).astype(np.float32))
+    assert all(len(set(row.tolist())) == ng for row in s.reshape(-1, ng))
+    return s
+
+
+def test_int4_gemv_group_scales_closed_form():
+    """gemv_f32 with a distinct scale per (row, group) against the dequantise-then-multiply closed
+    form sum_k q[n,k] * s[n, k // G] * x[k] in fp64 (np.repeat expands each scale over its group).
+    A scale indexed by k % n_groups (np.tile) instead of k // G misses by far more than rounding."""
+    g = np.random.default_rng(11)
+    N, K, G = 48, 640, 128
+    packed = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sb = _distinct_group_scales(g, (N, K // G))
+    x = bf16.rnd(g.standard_normal(K).astype(np.float32))
+    s = bf16.to_f32(sb).astype(np.float64)
+    q = int4.codes(packed).astype(np.float64)
+    ref = (q * np.repeat(s, G, axis=-1)) @ x.astype(np.float64)
+    got = int4.gemv_f32(packed, sb, x, G).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2.0 ** -23 * np.abs(ref) + 1e-30)
+    wrong = (q * np.tile(s, (1, G))) @ x.astype(np.float64)
+    assert rel_l2(wrong, ref) > 0.1
+
+
+def test_int4_gemv_group_scales_brute_force_2x256():
+    """Two rows of 256 columns, two groups each, summed term by term in Python floats."""
+    g = np.random.default_rng(12)
+    packed = g.integers(0, 256, (2, 128), dtype=np.uint8)
+    sb = _distinct_group_scales(g, (2, 2))
+    x = bf16.rnd(g.standard_normal(256).astype(np.float32))
+    got = int4.gemv_f32(packed, sb, x, 128)
+    for n in range(2):
+        acc = 0.0
+        for k in range(256):
+            byte = int(packed[n, k // 2])
+            nib = (byte & 0xF) if k % 2 == 0 else (byte >> 4)
+            scale = float(bf16.to_f32(np.array([sb[n, k // 128]], np.uint16))[0])
+            acc += (nib - 8) * scale * float(x[k])
+        assert abs(float(got[n]) - acc) <= 2.0 ** -23 * abs(acc) + 1e-30
+
+
+def test_int4_ffn_group_scales_against_fp64_dequantised_ffn():
+    """ffn with distinct group scales against the reference's _ref_ffn semantics
+    (moe_kernel.py:117-125, dequantise then fp64 products) written on dequantised matrices;
+    the reference's own criterion max|err| / max|ref| < 2e-2, and the rel-L2 bar of the path."""
+    g = np.random.default_rng(13)
+    E, H, I = 3, 512, 256
+    x = bf16.rnd(g.standard_normal(H).astype(np.float32))
+    rw = bf16.rnd(np.array([0.5, 0.3, 0.2], np.float32))
+    experts, ref = [], np.zeros(H, np.float64)
+    for e in range(E):
+        gq = g.integers(0, 256, (2 * I, H // 2), dtype=np.uint8)
+        dq = g.integers(0, 256, (H, I // 2), dtype=np.uint8)
+        gs = _distinct_group_scales(g, (2 * I, H // 128))
+        ds = _distinct_group_scales(g, (H, I // 128))
+        experts.append((gq, gs, dq, ds))
+        wg = int4.codes(gq) * np.repeat(bf16.to_f32(gs).astype(np.float64), 128, axis=-1)
+        wd = int4.codes(dq) * np.repeat(bf16.to_f32(ds).astype(np.float64), 128, axis=-1)
+        gu = torch.from_numpy(wg @ x.astype(np.float64))
+        a = F.silu(gu[:I]) * gu[I:]
+        ref += float(rw[e]) * (wd @ a.numpy())
+    got = int4.ffn(x, experts, rw, 128).astype(np.float64)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 2e-2
+    assert rel_l2(got, ref) < 5e-3
+
+
 def test_int4_ambiguous_roundings_known_answers():
     v = np.array([1.12109375 + 1e-7, 1.12107, 1.5, -1.12109375 - 2e-7, 3.0, 1.0], np.float32)
     idx, other, dist = int4.ambiguous_roundings(v, 2e-6)
