@@ -48,6 +48,7 @@ enum tmoe_status {
   TMOE_ERR_HIP = -5,        /* a HIP runtime call or kernel launch failed          */
   TMOE_ERR_EXPERT_ID = -6,  /* device saw an expert id outside [0, E] (sentinel E is skipped) */
   TMOE_ERR_TIMEOUT = -7,    /* a kernel's bounded dependency wait expired (results invalid)   */
+  TMOE_ERR_SCRATCH = -8,    /* the call needs more than TMOE_STATIC_SCRATCH_BYTES (no-alloc entry point) */
 };
 
 /* ABI version of the loaded library (TMOE_ABI_VERSION at build time). */
@@ -190,6 +191,32 @@ int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float eps, const
                         const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E, int I,
                         int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                         void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------- allocation-free block
+ * No counterpart in the reference.  For callers that cannot allocate device memory or
+ * pass a workspace (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tmoe_moe_block_bf16 with the workspace replaced by a static
+ * device array inside the library, TMOE_STATIC_SCRATCH_BYTES per GPU, held by each GPU
+ * the library runs on until the process ends.  Nothing is allocated by the call.
+ *   - Calls needing a larger workspace than the static one (tmoe_workspace_bytes(T, ...)
+ *     > TMOE_STATIC_SCRATCH_BYTES; at H=2560, E=256, I=Is=1024, k=8 that is T > 221)
+ *     return TMOE_ERR_SCRATCH before any launch.
+ *   - `status`: a caller-owned device uint32 (4-byte aligned, required) into which the
+ *     kernels OR device-detected conditions: 1 = an expert id outside [0, E] (cannot come
+ *     from the router itself), 2 = a bounded wait expired (results invalid).  The caller
+ *     zeroes it and reads it at its own synchronisation points.
+ *   - `stream` must belong to the current device (else TMOE_ERR_HIP); the scratch is that
+ *     device's copy.
+ *   - Every call on one GPU shares that GPU's scratch: calls that overlap in time on one
+ *     GPU (other streams, other threads) race and must be ordered by the caller.
+ * Arguments otherwise as tmoe_moe_block_bf16; results bit-identical to it.
+ */
+#define TMOE_STATIC_SCRATCH_BYTES (16u << 20)
+int tmoe_moe_block_bf16_noalloc(const void* x, int T, const void* router_w, const float* logits_in,
+                                const uint64_t* expert_table, const void* sh_gate, const void* sh_up,
+                                const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k, int Is,
+                                void* out, int64_t* ids_out, void* weights_out, uint32_t* heat, uint32_t* status,
+                                void* stream);
 
 /* ---------------------------------------------------------------- route telemetry (a13)
  * The reference's per-layer route-reuse counters (tarfa/engine/fused_int4.py:71-95

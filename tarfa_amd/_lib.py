@@ -38,6 +38,8 @@ SIGNATURES = {
                                  _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tmoe_moe_layer_int4": (_i, [_vp, _i, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                  _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tmoe_moe_block_bf16_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                         _vp, _vp, _vp, _vp, _vp, _vp]),
     "tmoe_route_telemetry_bytes": (_sz, [_i, _i, _i]),
     "tmoe_route_record": (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
 }

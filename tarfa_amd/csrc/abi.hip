@@ -1,6 +1,8 @@
 // extern "C" entry points: argument validation, workspace carving, launches.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "tmoe_device.h"
 #include "tmoe_ws.h"
 #include "tmoe_decode.h"
@@ -14,7 +16,7 @@ int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64,
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s, bool q4, const uint16_t* resid);
+                   void* ws, hipStream_t s, bool q4, const uint16_t* resid, uint32_t* err);
 int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
 int rmsnorm_launch(const uint16_t* h, const uint16_t* w, float eps, int T, int H, uint16_t* x, hipStream_t s);
 int residual_add_launch(const uint16_t* h, uint16_t* y, size_t n, hipStream_t s);
@@ -60,6 +62,7 @@ extern "C" const char* tmoe_strerror(int status) {
     case TMOE_ERR_HIP: return "HIP runtime call or kernel launch failed";
     case TMOE_ERR_EXPERT_ID: return "expert id outside [0, num_experts] seen on the device";
     case TMOE_ERR_TIMEOUT: return "a bounded device-side dependency wait expired";
+    case TMOE_ERR_SCRATCH: return "the call needs more scratch than the library's static scratch holds";
     default: return "unknown tmoe status";
   }
 }
@@ -83,6 +86,7 @@ extern "C" int tmoe_workspace_status(void* workspace, void* stream) {
 
 static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
   p.status = ws_ptr<uint32_t>(ws, L.status);
+  p.err = p.status + kStatusError;
   p.logits_ws = ws_ptr<float>(ws, L.logits);
   p.ids_ws = ws_ptr<int32_t>(ws, L.ids);
   p.w_ws = ws_ptr<float>(ws, L.wts);
@@ -124,7 +128,8 @@ static int experts_forward(const void* x, int T, const int64_t* ids, const void*
     return q4 ? decode_fused_launch(p, false, s) : decode(p, false, s);
   }
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
-                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4, nullptr);
+                        nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4, nullptr,
+                        nullptr);
 }
 
 extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
@@ -147,7 +152,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
                      const void* sh_gate, const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E,
                      int I, int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                      void* workspace, size_t ws_bytes, hipStream_t s, bool q4, const void* ln_w = nullptr,
-                     float ln_eps = 0.f) {
+                     float ln_eps = 0.f, uint32_t* err = nullptr) {
   const bool has_sh = sh_gate || sh_up || sh_down || sh_gate_w;
   if (has_sh && (!sh_gate || !sh_up || !sh_down || !sh_gate_w || Is < 8)) return TMOE_ERR_NULL;
   if (!has_sh) Is = 0;
@@ -178,6 +183,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     p.w_out = (uint16_t*)weights_out;
     p.heat = heat;
     bind_ws(p, workspace, L);
+    if (err) p.err = err;
     if (!ln_w) return q4 ? decode_fused_launch(p, true, s) : decode(p, true, s);
     // The fused kernel forms the normalised input in every task and adds the residual in
     // its combine; other shapes normalise first and add the residual after.
@@ -215,7 +221,7 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     if (int st = launch_shared_gate((const uint16_t*)x, (const uint16_t*)sh_gate_w, T, H, gs, s)) return st;
   return prefill_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
                         (const uint16_t*)sh_up, (const uint16_t*)sh_down, has_sh ? gs : nullptr, H, E, I, k, Is,
-                        (uint16_t*)out, workspace, s, q4, ln_w ? (const uint16_t*)h : nullptr);
+                        (uint16_t*)out, workspace, s, q4, ln_w ? (const uint16_t*)h : nullptr, err);
 }
 
 extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, const float* logits_in,
@@ -255,4 +261,52 @@ extern "C" int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float
   if (!ln_w) return TMOE_ERR_NULL;
   return moe_block(h, T, router_w, logits_in, expert_table_q4, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
                    out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, true, ln_w, eps);
+}
+
+// ---------------------------------------------------------------- allocation-free block
+// The workspace of tmoe_moe_block_bf16_noalloc is this file-scope device array; each GPU
+// holds its own copy (at its own address) for the life of the process.  Host code never
+// names it as memory: the first call on a device, with that device current, looks up
+// that device's copy with hipGetSymbolAddress and keeps the pointer, and only that
+// pointer reaches the kernels.  The array is zero when the code object loads, and every
+// call leaves what the next one needs at zero (sync counters) or harmless (tagged
+// hand-off words carry the epoch of the call that wrote them), as with a caller's
+// workspace; the T-dependent regions are written before they are read within a call.
+static __device__ __align__(256) unsigned char scratch[TMOE_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+}  // namespace
+
+// This device's copy of the scratch array, or nullptr if the lookup fails.
+static void* device_scratch(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch[dev] = ptr;
+  }
+  return g_scratch[dev];
+}
+
+extern "C" int tmoe_moe_block_bf16_noalloc(const void* x, int T, const void* router_w, const float* logits_in,
+                                           const uint64_t* expert_table, const void* sh_gate, const void* sh_up,
+                                           const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k,
+                                           int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                           uint32_t* status, void* stream) {
+  if (!status) return TMOE_ERR_NULL;
+  if ((uintptr_t)status & 3u) return TMOE_ERR_ALIGN;
+  const int has_sh = sh_gate || sh_up || sh_down || sh_gate_w;
+  if (int st = check_shape(T, H, E, I, k, has_sh ? Is : 0)) return st;
+  if (ws_layout(T, H, E, I, k, has_sh ? Is : 0).total > (size_t)TMOE_STATIC_SCRATCH_BYTES) return TMOE_ERR_SCRATCH;
+  hipStream_t s = (hipStream_t)stream;
+  int dev = -1, sdev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TMOE_ERR_HIP;
+  if (s && (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev)) return TMOE_ERR_HIP;
+  void* ws = device_scratch(dev);
+  if (!ws) return TMOE_ERR_HIP;
+  return moe_block(x, T, router_w, logits_in, expert_table, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, out,
+                   ids_out, weights_out, heat, ws, (size_t)TMOE_STATIC_SCRATCH_BYTES, s, false, nullptr, 0.f, status);
 }

@@ -27,7 +27,7 @@ constexpr int kDownRowsPerBlock = 4 * kDownRowsPerWave;
 __device__ __forceinline__ bool slot_expert(const DecodeParams& p, int j, int& e) {
   e = p.ids_in ? (int)p.ids_in[j] : p.ids_ws[j];
   if (e >= 0 && e < p.E) return true;
-  if (e != p.E && p.status) atomicOr(p.status + kStatusError, 1u);   // sentinel E is a silent skip
+  if (e != p.E && p.err) atomicOr(p.err, 1u);   // sentinel E is a silent skip
   return false;
 }
 __device__ __forceinline__ float slot_weight(const DecodeParams& p, int j) {

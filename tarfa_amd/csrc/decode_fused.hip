@@ -892,7 +892,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   constexpr int RQ = q4_down_rows(MI);
   const int lane0 = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint32_t* err = p.status + kStatusError;
+  uint32_t* err = p.err;
   const int q = (int)(blockIdx.x % 8) * kWaves + wid;
   uint32_t* queue = line(p, kLnQueue + q);
   const uint32_t users = (gridDim.x - (uint32_t)(q / kWaves) + 7u) / 8u;

@@ -62,7 +62,7 @@ int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, fl
 // (desc non-null) one descriptor per M-chunk: {group, rows, first row in group order, 0}.
 __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, const int64_t* ids64, int T, int k,
                                                          int E, int shared_rows, int32_t* offsets,
-                                                         int32_t* tile_start, int32_t* inv, uint32_t* status,
+                                                         int32_t* tile_start, int32_t* inv, uint32_t* err,
                                                          int4* desc) {
   __shared__ int cnt[1024];
   const int tid = threadIdx.x;
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, c
       inv[j] = -1;
     }
   }
-  if (bad && status) atomicOr(status + kStatusError, 1u);
+  if (bad && err) atomicOr(err, 1u);
   __syncthreads();
   // Inclusive Hillis-Steele scans of counts and M-chunks (groups 0..E-1, then the shared group).
   const int c = tid < E ? cnt[tid] : 0;
@@ -954,11 +954,11 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
 
 // ---------------------------------------------------------------- driver
 int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, int E, int shared_rows,
-                    int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tile_start, uint32_t* status,
+                    int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tile_start, uint32_t* err,
                     hipStream_t s, int4* desc) {
   if ((long)T * k > kScatterMaxN) return TMOE_ERR_SHAPE;
   hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, s, ids32, ids64, T, k, E, shared_rows, offsets,
-                     tile_start, inv, status, desc);
+                     tile_start, inv, err, desc);
   hipLaunchKernelGGL(k_dispatch_scatter, dim3(E), dim3(1024), 0, s, ids32, ids64, T, k, offsets, perm, inv);
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
@@ -966,7 +966,7 @@ int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, in
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s, bool q4, const uint16_t* resid) {
+                   void* ws, hipStream_t s, bool q4, const uint16_t* resid, uint32_t* err) {
   const bool has_sh = sh_gate != nullptr;
   if (H % 128 || I % 64 || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
   if (q4 && I % 128) return TMOE_ERR_SHAPE;   // int4: every 64-wide K stage inside one 128-column group
@@ -975,12 +975,12 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   int32_t* perm = ws_ptr<int32_t>(ws, L.perm);
   int32_t* inv = ws_ptr<int32_t>(ws, L.inv);
   int32_t* tile_start = ws_ptr<int32_t>(ws, L.scratch);
-  uint32_t* status = ws_ptr<uint32_t>(ws, L.status);
+  if (!err) err = ws_ptr<uint32_t>(ws, L.status) + kStatusError;
   uint16_t* act = ws_ptr<uint16_t>(ws, L.act);
   uint16_t* ch = ws_ptr<uint16_t>(ws, L.ch);
   uint16_t* sh = ws_ptr<uint16_t>(ws, L.sh);
   int4* desc = ws_ptr<int4>(ws, L.desc);
-  if (int st = dispatch_launch(ids32, ids64, T, k, E, has_sh ? T : 0, offsets, perm, inv, tile_start, status, s,
+  if (int st = dispatch_launch(ids32, ids64, T, k, E, has_sh ? T : 0, offsets, perm, inv, tile_start, err, s,
                                desc))
     return st;
 
@@ -1070,5 +1070,5 @@ extern "C" int tmoe_dispatch(const int64_t* ids, int T, int k, int E, int32_t* o
   const Ws L = ws_layout(T, 8, E, 8, k, 0);
   if (ws_bytes < L.scratch + sizeof(int32_t) * (size_t)(E + 64)) return TMOE_ERR_WORKSPACE;
   return dispatch_launch(nullptr, ids, T, k, E, 0, offsets, perm, inv, ws_ptr<int32_t>(workspace, L.scratch),
-                         ws_ptr<uint32_t>(workspace, L.status), (hipStream_t)stream, nullptr);
+                         ws_ptr<uint32_t>(workspace, L.status) + kStatusError, (hipStream_t)stream, nullptr);
 }

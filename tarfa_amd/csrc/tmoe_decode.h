@@ -28,7 +28,8 @@ struct DecodeParams {
   uint16_t* w_out;            // optional
   float* logits_out;          // optional
   uint32_t* heat;             // optional
-  uint32_t* status;           // workspace
+  uint32_t* status;           // workspace status block
+  uint32_t* err;              // device-detected error bits (kErrExpertId | kErrTimeout) are OR-ed here
   float* logits_ws;           // [E + 1]
   int32_t* ids_ws;            // [k]
   float* w_ws;                // [k]

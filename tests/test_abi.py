@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_strerror():
     lib = _lib.lib()
     assert lib.tmoe_abi_version() == _lib.ABI_VERSION
-    for code in (0, -1, -2, -3, -4, -5, -6):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8):
         assert lib.tmoe_strerror(code).decode() != "unknown tmoe status"
     assert lib.tmoe_strerror(-99).decode() == "unknown tmoe status"
 
