@@ -236,6 +236,19 @@ size_t tmoe_route_telemetry_bytes(int L, int k, int E);
 int tmoe_route_record(const int64_t* ids, int L, int k, int E, void* state, size_t state_bytes,
                       void* stream);
 
+/* ---------------------------------------------------------------- debug timeline
+ * No counterpart in the reference (its decode is timed by wall clock around the whole call,
+ * tarfa/engine/fused_int4.py:164, 203-204).  While set, every batch-1 call that runs the
+ * fused decode kernel records, in the device buffer `buf` (8-byte aligned), the
+ * s_memrealtime stamps (100 MHz) of each of its tasks: 16 header words {tasks, blocks,
+ * router, shared up, shared down, gate/up per slot, down per slot, k, ...}, then per task
+ * {start, routing known, loads returned, end, HW_ID, XCC_ID, ticket, 0}, then per wave
+ * {entry, exit}, all uint64.  A launch whose records do not fit in `bytes` records nothing;
+ * each launch overwrites the last.  buf = NULL turns it off.  Process-wide; for profiling,
+ * not for concurrent use.
+ */
+int tmoe_debug_decode_trace(void* buf, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

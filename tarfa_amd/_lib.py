@@ -42,6 +42,7 @@ SIGNATURES = {
                                          _vp, _vp, _vp, _vp, _vp, _vp]),
     "tmoe_route_telemetry_bytes": (_sz, [_i, _i, _i]),
     "tmoe_route_record": (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
+    "tmoe_debug_decode_trace": (_i, [_vp, _sz]),
 }
 
 _LIB = None

@@ -56,11 +56,13 @@
 //   - The last wave to leave a queue re-zeroes its exit count; the last queue to
 //     drain advances the epoch.
 // Reference: tarfa/engine/fused_int4.py:163-205; transformers/.../modeling_qwen3_5_moe.py:715-717, 768-798.
+
 #include <mutex>
 
 #include "tmoe_decode.h"
 #include "tmoe_gemv.h"
 #include "tmoe_q4.h"
+#include "tmoe_topk.h"
 #include "tmoe_ws.h"
 
 namespace tmoe {
@@ -114,6 +116,7 @@ __device__ __forceinline__ void st128c(uint64_t* p, uint64_t a, uint64_t b) {
 __device__ __forceinline__ uint32_t add32c(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
 // A wave-uniform load of memory that no task writes during the call (expert
 // table, caller-supplied routing): through the constant address space it is a
 // scalar load, so waiting for it never waits for this wave's outstanding
@@ -192,6 +195,9 @@ __device__ __forceinline__ void load_acts(XPack<MAXC>& f, const uint64_t* w, int
     if (!b2.step(err)) return;
   }
 }
+
+// The copy of the logits a block reads: one of kLogitReplicas (16 blocks per copy).
+__device__ __forceinline__ int logit_copy(const DecodeParams& p) { return (int)(blockIdx.x % kLogitReplicas); }
 
 // Routing as seen by one block: the route words (lane layout of RouteWord), set once
 // (valid) by the block's resolving wave (poller).
@@ -355,122 +361,6 @@ __device__ __forceinline__ void down_q4(const uint8_t* dq, const uint16_t* ds, c
   }
 }
 
-// ---------------------------------------------------------------- top-8 selection
-// Exact top-8 of up to 256 logits (4 per lane), logit descending, ties to the lower
-// expert index, as one wave: each candidate becomes a 64-bit key (order-preserving
-// logit bits, then the inverted index; 0 = absent, -inf or NaN, never selected), each
-// lane sorts its 4 keys, then 6 bitonic merge levels over lane groups of 2 .. 64 keep
-// a sorted top-8 in every lane pair (even lane: ranks 0-3, odd lane: ranks 4-7).
-// Cross-lane steps are DPP moves (or one ds_bpermute at the two widest levels), so the
-// dependency chain is a few dozen instructions long rather than 8 rounds of wave-wide
-// max, ballot and readlane.
-__device__ __forceinline__ uint64_t topk_key(float v, int e) {
-  if (!(v > -INFINITY)) return 0ull;                     // -inf, NaN
-  uint32_t b = __float_as_uint(v);
-  if (b == 0x80000000u) b = 0u;                          // -0 ties with +0
-  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((uint64_t)o << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
-}
-__device__ __forceinline__ float topk_logit(uint64_t key) {
-  const uint32_t o = (uint32_t)(key >> 32);
-  return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
-}
-__device__ __forceinline__ void ce_desc(uint64_t& a, uint64_t& b) {
-  const bool sw = b > a;
-  const uint64_t hi = sw ? b : a, lo = sw ? a : b;
-  a = hi;
-  b = lo;
-}
-// The key of lane (lane ^ (2^LEVEL - 1)).
-template <int LEVEL>
-__device__ __forceinline__ uint64_t mirror_key(uint64_t k) {
-  int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
-  if constexpr (LEVEL == 1) {
-    lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, true);      // quad_perm [1,0,3,2]
-    hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, true);
-  } else if constexpr (LEVEL == 2) {
-    lo = __builtin_amdgcn_mov_dpp(lo, 0x1B, 0xF, 0xF, true);      // quad_perm [3,2,1,0]
-    hi = __builtin_amdgcn_mov_dpp(hi, 0x1B, 0xF, 0xF, true);
-  } else if constexpr (LEVEL == 3) {
-    lo = __builtin_amdgcn_mov_dpp(lo, kDppHalfMirror, 0xF, 0xF, true);
-    hi = __builtin_amdgcn_mov_dpp(hi, kDppHalfMirror, 0xF, 0xF, true);
-  } else if constexpr (LEVEL == 4) {
-    lo = __builtin_amdgcn_mov_dpp(lo, kDppMirror, 0xF, 0xF, true);
-    hi = __builtin_amdgcn_mov_dpp(hi, kDppMirror, 0xF, 0xF, true);
-  } else {
-    const int src = ((int)(threadIdx.x & 63) ^ ((1 << LEVEL) - 1)) * 4;
-    lo = __builtin_amdgcn_ds_bpermute(src, lo);
-    hi = __builtin_amdgcn_ds_bpermute(src, hi);
-  }
-  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
-}
-__device__ __forceinline__ void clean4(uint64_t (&k)[4]) {
-  ce_desc(k[0], k[2]);
-  ce_desc(k[1], k[3]);
-  ce_desc(k[0], k[1]);
-  ce_desc(k[2], k[3]);
-}
-template <int LEVEL>
-__device__ __forceinline__ void merge_level(uint64_t (&k)[4], bool odd) {
-  uint64_t c[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint64_t pk = mirror_key<LEVEL>(k[3 - i]);
-    // Level 1 splits the 8 keys of a lane pair (upper half to the even lane); wider
-    // levels keep the upper half of the two halves' top-8s in both halves.
-    c[i] = (LEVEL == 1 && odd) ? (pk < k[i] ? pk : k[i]) : (pk > k[i] ? pk : k[i]);
-  }
-  if constexpr (LEVEL > 1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint64_t q = mirror_key<1>(c[i]);
-      c[i] = odd ? (q < c[i] ? q : c[i]) : (q > c[i] ? q : c[i]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) k[i] = c[i];
-  clean4(k);
-}
-// Lane r < k gets slot r's expert id (E when fewer than r + 1 candidates exist) and
-// logit; every lane gets the largest logit in m (0 when none).
-__device__ __forceinline__ void top8_bitonic(const float (&v)[4], int E, int k, int lane, int& my_id,
-                                             float& my_lw, float& m) {
-  uint64_t key[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = e < E ? topk_key(v[i], e) : 0ull;
-  }
-  ce_desc(key[0], key[1]);
-  ce_desc(key[2], key[3]);
-  ce_desc(key[0], key[2]);
-  ce_desc(key[1], key[3]);
-  ce_desc(key[1], key[2]);
-  const bool odd = lane & 1;
-  merge_level<1>(key, odd);
-  merge_level<2>(key, odd);
-  merge_level<3>(key, odd);
-  merge_level<4>(key, odd);
-  merge_level<5>(key, odd);
-  merge_level<6>(key, odd);
-  // Rank r lives in lane r >> 2, register r & 3.
-  const int src = (lane >> 2) & 1;
-  uint64_t mine = 0ull;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int lo = __builtin_amdgcn_ds_bpermute(src * 4, (int)(uint32_t)key[j]);
-    const int hi = __builtin_amdgcn_ds_bpermute(src * 4, (int)(uint32_t)(key[j] >> 32));
-    if ((lane & 3) == j) mine = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
-  }
-  const uint64_t top = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key[0] >> 32), 0) << 32) |
-                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], 0);
-  m = top ? topk_logit(top) : 0.f;
-  if (lane < k && lane < 8 && mine) {
-    my_id = (int)(0xFFFFFFFFu - (uint32_t)mine);
-    my_lw = topk_logit(mine);
-  }
-}
-
 // A block's routing: one wave of the block gathers every tagged logit of the block's copy,
 // selects the top-k, computes the softmax weights and the shared gate, and writes the
 // route words to LDS for the whole block.  Every block resolves the routing itself: the
@@ -481,7 +371,7 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
                                               RouteLds& L) {
   const bool has_sh = p.sh_gate != nullptr;
   __builtin_amdgcn_s_setprio(3);   // the routing gates every expert task: issue ahead of streaming waves
-  const uint64_t* lg = p.lg64 + (size_t)(blockIdx.x % kLogitReplicas) * p.lg_stride;
+  const uint64_t* lg = p.lg64 + (size_t)logit_copy(p) * p.lg_stride;
   float v[MAXEPL];
   float gl = 0.f;
   if (p.logits_in) {
@@ -491,6 +381,9 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
       v[i] = e < p.E ? p.logits_in[min(e, p.E - 1)] : -INFINITY;
     }
   }
+  const uint64_t ts_entry = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  uint64_t ts_ok = 0;
+  uint32_t rounds = 0;
   if (!p.logits_in || has_sh) {
     // Every load of a poll round is issued before any is waited for: the
     // addresses are clamped into the logit words, never skipped.
@@ -510,9 +403,11 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
           v[i] = in ? __uint_as_float((uint32_t)w[i]) : -INFINITY;
         }
       }
+      ++rounds;
       if (__all(ok)) break;
       if (!b.step(err)) break;
     }
+    if (p.trace) ts_ok = __builtin_amdgcn_s_memrealtime();
   }
   int my_id = p.E;          // lane r < k: slot r's expert and logit
   float my_lw = -INFINITY;
@@ -565,6 +460,7 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
       if (r == 0) m = g;
     }
   }
+  const uint64_t ts_sel = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
   // Softmax over all E in fp32 (max-subtracted), renormalised over the k
   // selected, rounded to bf16 -- one slot per lane.
   float ls = 0.f;
@@ -582,10 +478,21 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
   const uint32_t wsrc = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane - kRwW) & 63) * 4, (int)wb);
   const uint32_t gate = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
   const uint32_t word = lane < kRwW ? (uint32_t)my_id : lane < kRwGate ? wsrc : gate;
+  const uint64_t ts_soft = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
   if (lane < kRouteWords) L.word[lane] = word;
   __threadfence_block();
   if (lane == 0) __hip_atomic_store(&L.valid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   __builtin_amdgcn_s_setprio(0);
+  if (p.trace && lane == 0) {
+    uint64_t* rec = p.trace + kTraceHeader + (size_t)p.n_tasks * kTraceTaskWords + 2 * (size_t)gridDim.x * 4 +
+                    8 * (size_t)blockIdx.x;
+    rec[0] = ts_entry;
+    rec[1] = ts_ok;
+    rec[2] = __builtin_amdgcn_s_memrealtime();
+    rec[3] = rounds;
+    rec[4] = ts_sel;
+    rec[5] = ts_soft;
+  }
 }
 
 // The wave's routing cache `rwc` (lane l < kRouteWords holds route word l) from the
@@ -620,7 +527,7 @@ __device__ __forceinline__ void publish_routing(const DecodeParams& p, int lane,
     if (p.heat && rwc < (uint32_t)p.E) atomicAdd(p.heat + rwc, 1u);
   }
   if (p.logits_out) {
-    const uint64_t* lg = p.lg64 + (size_t)(blockIdx.x % kLogitReplicas) * p.lg_stride;
+    const uint64_t* lg = p.lg64 + (size_t)logit_copy(p) * p.lg_stride;
     for (int e = lane; e < p.E; e += 64)
       p.logits_out[e] = p.logits_in ? p.logits_in[e] : __uint_as_float((uint32_t)ld64c(lg + e));
   }
@@ -835,6 +742,8 @@ struct TaskRef {
   int type, slot, idx;
 };
 
+
+
 // Task t of the list R, then per slot j: Gj, D(j - kDownLag) once j >= kDownLag,
 // S after G(sh_after) and SD after G(sd_after); then the remaining D.  Pure arithmetic on values
 // held in scalar registers: a lookup table in kernel-argument memory costs a
@@ -882,17 +791,31 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
 // is the hidden state before the layer's RMSNorm (every task that loads x forms it) and
 // the combine adds the residual; without LN both pointers are null constants here, so
 // none of that code is in the kernel.
-template <int MH, int MI, bool EXACT, bool Q4, bool LN>
+// TRACE: the debug-timeline instantiation (exact-fit block shapes only); without it the
+// pointer is a null constant and no recording code or state is in the kernel.
+template <int MH, int MI, bool EXACT, bool Q4, bool LN, bool TRACE = false>
 __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   static_assert(!Q4 || EXACT, "int4 variants need H and I multiples of 512");
   if constexpr (!LN) {
     p.ln_w = nullptr;
     p.resid = nullptr;
   }
+  if constexpr (!TRACE) p.trace = nullptr;
   constexpr int RQ = q4_down_rows(MI);
   const int lane0 = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint32_t* err = p.err;
+  {
+    // Bring every 64-byte line of the kernel arguments into the scalar cache in one round
+    // trip: the compiler reads fields where it first needs them, and a field on a line not
+    // yet cached costs a memory round trip of its own before the first task can start.
+    typedef const __attribute__((address_space(4))) uint32_t ka_u32;
+    ka_u32* ka = (ka_u32*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t touch = 0;
+#pragma unroll
+    for (int o = 0; o < (int)(sizeof(DecodeParams) / 4); o += 16) touch ^= ka[o];
+    if (touch == 0x9E3779B9u && threadIdx.x == 0x3FF) err = nullptr;   // never taken: only makes the loads needed
+  }
   const int q = (int)(blockIdx.x % 8) * kWaves + wid;
   uint32_t* queue = line(p, kLnQueue + q);
   const uint32_t users = (gridDim.x - (uint32_t)(q / kWaves) + 7u) / 8u;
@@ -906,6 +829,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     s_rt.poller = 0u;
   }
   __syncthreads();
+
   uint32_t rwc = kUnseenWord;   // this wave's routing cache (lane layout of RouteWord)
   bool routed = p.ids_in != nullptr;
   if (p.ids_in) {
@@ -945,9 +869,19 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     }
   }
   uint32_t ticket = rank;
+  const uint64_t t_entry = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  if (p.trace && blockIdx.x == 0 && wid == 0 && lane0 == 0) {
+    const uint64_t hdr[kTraceHeader] = {(uint64_t)p.n_tasks, gridDim.x, (uint64_t)p.n_r, (uint64_t)p.n_s,
+                                        (uint64_t)p.n_sd, (uint64_t)p.n_g, (uint64_t)p.n_d, (uint64_t)p.k,
+                                        (uint64_t)p.sh_after, (uint64_t)p.sd_after, (uint64_t)kDownLag,
+                                        (uint64_t)p.q4, 0, 0, 0, 0};
+    for (int i = 0; i < kTraceHeader; ++i) p.trace[i] = hdr[i];
+  }
   for (uint32_t i = 0;; ++i) {
     const int t = q + kQueues * (int)ticket;
     if (t >= p.n_tasks) break;
+    uint64_t ts_start = 0, ts_route = 0, ts_take = 0;
+    if (p.trace) ts_start = __builtin_amdgcn_s_memrealtime();
     // The next ticket: drawn now from the queue's counter (first tickets are the
     // ranks), read after this task.  Vector memory returns in issue order, so the
     // task's own loads bring the draw back with them.
@@ -960,6 +894,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         nt = (uint32_t)__builtin_amdgcn_readlane((int)nxt, 0);
         got = true;
       }
+      if (p.trace && !ts_take) ts_take = __builtin_amdgcn_s_memrealtime();
     };
     if (DYN && lane0 == 0) {
       // An opaque (per-lane) address keeps this one lane's atomic as it is: the
@@ -979,6 +914,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       // wave or another of the block (one call site: the resolution is long code).
       route_fetch(p, lane, rwc, tag, err, s_rt);
       routed = true;
+      if (p.trace) ts_route = __builtin_amdgcn_s_memrealtime();
       if (t == p.n_r) publish_routing(p, lane, rwc);   // task n_r: the first gate/up task of slot 0
     }
     if (tk.type == kTR) {
@@ -1042,7 +978,23 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       asm volatile("" : "+v"(v));
       nt = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
     }
+    if (p.trace && lane0 == 0) {
+      uint64_t* rec = p.trace + kTraceHeader + (size_t)t * kTraceTaskWords;
+      rec[0] = ts_start;
+      rec[1] = ts_route;
+      rec[2] = ts_take;
+      rec[3] = __builtin_amdgcn_s_memrealtime();
+      rec[4] = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_ID
+      rec[5] = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 20);   // XCC_ID
+      rec[6] = ticket;
+      rec[7] = (uint64_t)tk.type | (uint64_t)(tk.slot + 1) << 8 | (uint64_t)tk.idx << 16;
+    }
     ticket = DYN ? users + nt : rank + users * (i + 1);
+  }
+  if (p.trace && lane0 == 0) {
+    uint64_t* rec = p.trace + kTraceHeader + (size_t)p.n_tasks * kTraceTaskWords + 2 * ((size_t)blockIdx.x * kWaves + wid);
+    rec[0] = t_entry;
+    rec[1] = __builtin_amdgcn_s_memrealtime();
   }
   // The last wave to leave queue q re-zeroes its exit count; the last queue to
   // drain ends the call.
@@ -1108,6 +1060,20 @@ static FusedKernel pick_fused_t(int H, int I, int Is, bool q4) {
 static FusedKernel pick_fused(int H, int I, int Is, bool q4, bool ln) {
   return ln ? pick_fused_t<true>(H, I, Is, q4) : pick_fused_t<false>(H, I, Is, q4);
 }
+// The recording twin of a block-mode exact-fit kernel, or null.
+static FusedKernel pick_traced(int H, int I, int Is, bool q4, bool ln) {
+  if (ln || H % 512 || I % 512 || (Is != 0 && Is != I)) return nullptr;
+  switch ((H / 512) * 10 + I / 512) {
+    case 11: return q4 ? k_decode_fused<1, 1, true, true, false, true> : nullptr;
+    case 21: return q4 ? k_decode_fused<2, 1, true, true, false, true> : k_decode_fused<2, 1, true, false, false, true>;
+    case 22: return q4 ? k_decode_fused<2, 2, true, true, false, true> : k_decode_fused<2, 2, true, false, false, true>;
+    case 42: return q4 ? k_decode_fused<4, 2, true, true, false, true> : k_decode_fused<4, 2, true, false, false, true>;
+    case 52: return q4 ? k_decode_fused<5, 2, true, true, false, true> : k_decode_fused<5, 2, true, false, false, true>;
+    case 62: return q4 ? k_decode_fused<6, 2, true, true, false, true> : k_decode_fused<6, 2, true, false, false, true>;
+    case 84: return q4 ? k_decode_fused<8, 4, true, true, false, true> : k_decode_fused<8, 4, true, false, false, true>;
+  }
+  return nullptr;
+}
 
 // Blocks of a kernel to launch on the current device (cached): every one resident
 // at once, at most kBlocksPerCU per CU.
@@ -1132,6 +1098,11 @@ static int resident_blocks(FusedKernel k) {
   if (used < 64) cache[used++] = {dev, k, n};
   return n;
 }
+
+// The debug timeline buffer (tmoe_debug_decode_trace): process-wide, off (null) by default.
+static std::mutex g_trace_mu;
+static uint64_t* g_trace = nullptr;
+static size_t g_trace_bytes = 0;
 
 int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   const bool has_sh = p.sh_gate != nullptr;
@@ -1160,8 +1131,27 @@ int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   const int need = (p.n_tasks + kWaves - 1) / kWaves;
   if (grid > need) grid = need;
   if (grid < 8) grid = 8;   // every queue needs a wave
+  {
+    std::lock_guard<std::mutex> lock(g_trace_mu);
+    p.trace = g_trace && trace_words(p.n_tasks, grid * kWaves) * 8 <= g_trace_bytes ? g_trace : nullptr;
+  }
+  if (p.trace) {
+    FusedKernel kt = pick_traced(p.H, p.I, p.Is, p.q4 != 0, p.ln_w != nullptr);
+    if (kt && resident_blocks(kt) >= grid) k = kt;
+    else p.trace = nullptr;
+  }
   hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
 
 }  // namespace tmoe
+
+// Debug: every later fused-decode launch whose records fit in `bytes` writes its timeline
+// into the device buffer `buf` (each launch overwrites the last); null turns it off.
+extern "C" int tmoe_debug_decode_trace(void* buf, size_t bytes) {
+  if (buf && ((uintptr_t)buf & 7u)) return TMOE_ERR_ALIGN;
+  std::lock_guard<std::mutex> lock(tmoe::g_trace_mu);
+  tmoe::g_trace = static_cast<uint64_t*>(buf);
+  tmoe::g_trace_bytes = buf ? bytes : 0;
+  return TMOE_OK;
+}

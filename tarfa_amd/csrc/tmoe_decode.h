@@ -49,6 +49,19 @@ struct DecodeParams {
   int n_r, n_s, n_g, n_d, n_sd, n_tasks;   // task counts: router, shared up, gate/up per slot, down per slot,
                                            // shared down; total
   int sh_after, sd_after;     // shared gate/up (S) and shared down (SD) follow these slots' gate/up tasks
+  uint64_t* trace;            // debug timeline (tmoe_debug_decode_trace), or null: no records
 };
+
+// Debug timeline of one fused-decode call, in 100 MHz ticks of s_memrealtime:
+// a header of kTraceHeader words (written by the first wave), then kTraceTaskWords words per
+// task (start, routing known, loads returned, end, HW_ID, XCC_ID, ticket, type | (slot + 1) << 8 |
+// idx << 16), then two words
+// per wave (entry, exit), then eight per block (routing: poll start, logits complete, resolved,
+// poll rounds, top-k selected, weights formed, 0, 0).
+constexpr int kTraceHeader = 16;
+constexpr int kTraceTaskWords = 8;
+inline size_t trace_words(int n_tasks, int waves) {
+  return (size_t)kTraceHeader + (size_t)n_tasks * kTraceTaskWords + (size_t)waves * 2 + (size_t)waves * 2;
+}
 
 }  // namespace tmoe

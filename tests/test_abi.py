@@ -81,3 +81,9 @@ def test_entry_points_reject_bad_arguments_without_touching_the_device():
                   512, None, None, None, p, 1 << 30, None) == -3                        # ln_w alignment
     # T * k above 524288 (the dispatch's LDS mask)
     assert lib.tmoe_dispatch(p, 65537, 8, 16, p, p, p, p, 1 << 40, None) == -2
+
+
+def test_debug_trace_switch_checks_alignment_without_touching_the_device():
+    lib = _lib.lib()
+    assert lib.tmoe_debug_decode_trace(ctypes.c_void_p(0x1003), 4096) == -3   # TMOE_ERR_ALIGN
+    assert lib.tmoe_debug_decode_trace(None, 0) == 0
