@@ -169,6 +169,33 @@ int tmoe_moe_block_int4(const void* x, int T, const void* router_w, const float*
                         int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                         void* workspace, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- the reference's int4 files
+ * The int4 layout of the reference's own per-layer files (tarfa/engine/channel_q4.py:18,
+ * 28-38; moe_kernel.py:10-14): the same packed nibbles, but ONE fp16 scale per weight row
+ * (G = K), dequantised by the reference as fp16((nibble - 8) * s[n])
+ * (channel_q4.py:10-14 dequant_int4).
+ * tmoe_dequant_int4_f16: that dequantisation, bit for bit: fp16 scales [N, K/G], fp16 out
+ *   [N, K], G = K for the reference's per-row layout (any even G dividing K accepted).
+ *   packed 4-byte and out 16-byte aligned.
+ * tmoe_experts_forward_int4_f16rows / tmoe_moe_block_int4_f16rows: the int4 entry points
+ *   above with expert table uint64_t[E][4] = { gate_up packed [2I, H/2] u8, gate_up scales
+ *   [2I] fp16, down packed [H, I/2] u8, down scales [H] fp16 } (16-byte aligned).
+ *   T == 1: as the reference's moe_ffn (moe_kernel.py:90-104): per row, the fp32 sum of
+ *   (nibble - 8) * x times fp32(s); act = bf16(silu(g) * u) in fp32; fp32 down rows; fp32
+ *   router-order weighted sum; one bf16 cast.  T > 1: the exact-BF16 prefill on the weights
+ *   bf16((nibble - 8) * fp32(s)), the exact product rounded once (the reference's own int4
+ *   prefill multiplies in the model dtype, fused_int4.py:257-258).
+ */
+int tmoe_dequant_int4_f16(const void* packed, const void* scales, int N, int K, int G, void* out, void* stream);
+int tmoe_experts_forward_int4_f16rows(const void* x, int T, const int64_t* ids, const void* weights,
+                                      const uint64_t* expert_table_q4r, int H, int E, int I, int k, void* out,
+                                      void* workspace, size_t ws_bytes, void* stream);
+int tmoe_moe_block_int4_f16rows(const void* x, int T, const void* router_w, const float* logits_in,
+                                const uint64_t* expert_table_q4r, const void* sh_gate, const void* sh_up,
+                                const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k, int Is,
+                                void* out, int64_t* ids_out, void* weights_out, uint32_t* heat, void* workspace,
+                                size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------- the MoE sublayer
  * The steps on either side of the block in a Qwen3.5-MoE decoder layer
  * (transformers/models/qwen3_5_moe/modeling_qwen3_5_moe.py:870-875): h is the hidden

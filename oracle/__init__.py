@@ -14,7 +14,8 @@ moe     router (fp32 logits, softmax, top-k, renorm), dispatch permutation,
         exact-BF16 expert SwiGLU for decode and prefill, shared expert, combine.
 int4    builder-defined group-128 quantiser, dequantiser and the fused
         dequant-GEMV FFN semantics of the int4 fast mode, with the
-        enumeration of activations that sit on a bf16 rounding midpoint.
+        enumeration of activations that sit on a bf16 rounding midpoint; the
+        reference's own per-row fp16 layout (dequant, GEMV, FFN).
 telemetry  route-reuse counters of the reference's decode telemetry.
 cpu_reference  the reference's op chain in torch CPU bf16 (CPU baseline, pin).
 
@@ -38,5 +39,10 @@ Pinning status (each function is checked in ``tests/test_oracle.py`` and
 * int4 ffn            pinned: reference ``_ref_ffn`` closed form (``moe_kernel.py:117-125``)
                       reimplemented in torch fp64 with per-row scales (group = K).
 * int4 ffn_candidates pinned: known answers at bf16 midpoints; first candidate == ffn.
+* int4 dequant_f16    pinned: exhaustive 16 codes x every finite fp16 scale vs torch's fp16
+                      ``q.to(float16) * scale`` (channel_q4.py:10-14 run in torch CPU).
+* int4 gemv_rows / ffn_rows  pinned: the reference's ``_ref_ffn`` (moe_kernel.py:117-125) on
+                      fp16-dequantised weights in torch fp64, and a brute-force loop.
+* int4 dequant_rows_bf16     pinned: torch ``(q.float() * s.float()).to(bfloat16)``.
 * telemetry           pinned: a hand-worked sequence of steps (fused_int4.py:71-84).
 """

@@ -8,6 +8,9 @@ tarfa/engine/moe_kernel.py:10-14, tarfa/engine/channel_q4.py:10-14):
   dequant  w_hat = bf16(fp32((nibble - 8) * s[n, k // G]))   (the product is exact in
            fp32: at most 3 x 8 significant bits; only the bf16 rounding is inexact)
 
+The reference's own files carry ONE fp16 scale per row (channel_q4.py:10-14, 18, 28-38;
+moe_kernel.py:10-14); ``dequant_f16``, ``gemv_rows`` and ``ffn_rows`` restate that layout.
+
 The reference carries no quantiser (its int4 files come from outside the
 repository, channel_q4.py:6).  The quantiser here is this build's definition:
 
@@ -112,7 +115,7 @@ def ambiguous_roundings(v, rel):
     return idx, other[idx], dist[idx]
 
 
-def ffn_candidates(x, experts, rw, group=128, rel=2e-6, max_flips=6):
+def ffn_candidates(x, experts, rw, group=128, rel=2e-6, max_flips=6, gemv=None):
     """Every output ``ffn`` can give when each activation lying within ``rel`` of a bf16
     midpoint may round either way.
 
@@ -122,13 +125,16 @@ def ffn_candidates(x, experts, rw, group=128, rel=2e-6, max_flips=6):
     ulps of a bf16 midpoint can therefore legitimately round either way, and one such
     flip of a large activation moves every output row by ~1e-3 relative.  Returns a list
     of bf16 outputs (the first is ``ffn`` itself); at most ``max_flips`` of the closest
-    cases are enumerated.
+    cases are enumerated.  ``gemv`` (default: the group form ``gemv_f32``) takes (packed,
+    scales, vector); ``gemv_rows`` gives the candidates of ``ffn_rows``.
     """
+    if gemv is None:
+        gemv = lambda pk, sc, v: gemv_f32(pk, sc, v, group)  # noqa: E731
     x = np.asarray(x, np.float32)
     rw = np.asarray(rw, np.float32).reshape(-1)
     acts, flips = [], []
     for j, (gq, gs, dq, ds) in enumerate(experts):
-        gu = gemv_f32(gq, gs, x, group).astype(np.float64)
+        gu = gemv(gq, gs, x).astype(np.float64)
         inter = gu.shape[0] // 2
         a = _act_f64(gu[:inter], gu[inter:]).astype(np.float32)
         acts.append(rb(a))
@@ -143,7 +149,57 @@ def ffn_candidates(x, experts, rw, group=128, rel=2e-6, max_flips=6):
             for b, (_, jj, i, alt) in enumerate(flips):
                 if jj == j and (mask >> b) & 1:
                     act[i] = alt
-            d = gemv_f32(dq, ds, act, group).astype(np.float64)
+            d = gemv(dq, ds, act).astype(np.float64)
             y = (y + (d * np.float64(rw[j])).astype(np.float32)).astype(np.float32).astype(np.float64)
         outs.append(rb(y.astype(np.float32)))
     return outs
+
+
+# ------------------------------------------------------------------ the reference's per-row fp16 layout
+
+def f16_to_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def dequant_f16(packed, scale_bits, group):
+    """(packed, fp16 scale bits [N, K/G]) -> fp16 bit patterns [N, K]: channel_q4.py:10-14
+    ``q.to(torch.float16) * scale[:, None]`` (G = K: the reference's per-row scale), one
+    correctly rounded fp16 multiply of an exact code and an fp16 scale."""
+    q = codes(packed).astype(np.float16)
+    s = np.repeat(np.asarray(scale_bits, np.uint16).view(np.float16), group, axis=-1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (q * s).view(np.uint16)
+
+
+def gemv_rows(packed, scale_bits, x):
+    """The reference kernel's row: fp32 acc = sum_k (nibble - 8) x[k] (fp64 inside, rounded
+    to fp32), then y = fp32(acc * fp32(s[n])) (moe_kernel.py:54-63, per-row fp16 scale)."""
+    q = codes(packed).astype(np.float64)
+    acc = (q @ np.asarray(x, np.float64)).astype(np.float32)
+    return (acc * f16_to_f32(np.asarray(scale_bits).reshape(-1))).astype(np.float32)
+
+
+def ffn_rows(x, experts, rw):
+    """moe_ffn (moe_kernel.py:90-104) on the reference's per-row fp16 layout for one token:
+    ``experts`` = (gate_up_packed [2I, H/2], gate_up_scale [2I] fp16 bits, down_packed
+    [H, I/2], down_scale [H] fp16 bits) in router order, ``rw`` the bf16 routing weights.
+    act = bf16(silu(g) * u) in fp32 (:100; the engine dtype here is bf16), fp32 weighted
+    sum over experts in router order (:103), one cast to bf16 (:104)."""
+    x = np.asarray(x, np.float32)
+    y = np.zeros(x.shape[0], np.float32)
+    for (gq, gs, dq, ds), w in zip(experts, np.asarray(rw, np.float32).reshape(-1)):
+        gu = gemv_rows(gq, gs, x).astype(np.float64)
+        inter = gu.shape[0] // 2
+        act = rb(_act_f64(gu[:inter], gu[inter:]).astype(np.float32))
+        d = gemv_rows(dq, ds, act)
+        y = (y + (d * np.float32(w)).astype(np.float32)).astype(np.float32)
+    return rb(y)
+
+
+def dequant_rows_bf16(packed, scale_bits):
+    """The bf16 weights the exact-BF16 prefill uses for the per-row layout: the exact
+    product (nibble - 8) * fp32(s[n]) rounded once to bf16 (bit patterns)."""
+    q = codes(packed).astype(np.float32)
+    s = f16_to_f32(np.asarray(scale_bits).reshape(-1))[:, None]
+    with np.errstate(over="ignore"):
+        return bf16.bits(q * s)

@@ -43,6 +43,10 @@ SIGNATURES = {
     "tmoe_route_telemetry_bytes": (_sz, [_i, _i, _i]),
     "tmoe_route_record": (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
     "tmoe_debug_decode_trace": (_i, [_vp, _sz]),
+    "tmoe_dequant_int4_f16": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
+    "tmoe_experts_forward_int4_f16rows": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "tmoe_moe_block_int4_f16rows": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                         _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _LIB = None

@@ -16,7 +16,7 @@ int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64,
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s, bool q4, const uint16_t* resid, uint32_t* err);
+                   void* ws, hipStream_t s, int q4, const uint16_t* resid, uint32_t* err);
 int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
 int rmsnorm_launch(const uint16_t* h, const uint16_t* w, float eps, int T, int H, uint16_t* x, hipStream_t s);
 int residual_add_launch(const uint16_t* h, uint16_t* y, size_t n, hipStream_t s);
@@ -104,11 +104,11 @@ static void bind_ws(DecodeParams& p, void* ws, const Ws& L) {
 }
 
 
-// Int4 mode: group-128 scales; T == 1 needs H and I multiples of 512, T > 1 multiples of
-// 128; table entries 16-byte aligned.
+// Int4 modes (q4 = 1: group-128 bf16 scales; q4 = 2: the reference's per-row fp16 scales):
+// T == 1 needs H and I multiples of 512, T > 1 multiples of 128; table entries 16-byte aligned.
 static int experts_forward(const void* x, int T, const int64_t* ids, const void* weights,
                            const uint64_t* expert_table, int H, int E, int I, int k, void* out, void* workspace,
-                           size_t ws_bytes, hipStream_t s, bool q4) {
+                           size_t ws_bytes, hipStream_t s, int q4) {
   if (int st = check_shape(T, H, E, I, k, 0)) return st;
   if (!x || !ids || !weights || !expert_table || !out || !workspace) return TMOE_ERR_NULL;
   if (misaligned(x) || misaligned(workspace)) return TMOE_ERR_ALIGN;
@@ -136,14 +136,21 @@ extern "C" int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* id
                                          const uint64_t* expert_table, int H, int E, int I, int k, void* out,
                                          void* workspace, size_t ws_bytes, void* stream) {
   return experts_forward(x, T, ids, weights, expert_table, H, E, I, k, out, workspace, ws_bytes, (hipStream_t)stream,
-                         false);
+                         0);
 }
 
 extern "C" int tmoe_experts_forward_int4(const void* x, int T, const int64_t* ids, const void* weights,
                                          const uint64_t* expert_table_q4, int H, int E, int I, int k, void* out,
                                          void* workspace, size_t ws_bytes, void* stream) {
   return experts_forward(x, T, ids, weights, expert_table_q4, H, E, I, k, out, workspace, ws_bytes,
-                         (hipStream_t)stream, true);
+                         (hipStream_t)stream, 1);
+}
+
+extern "C" int tmoe_experts_forward_int4_f16rows(const void* x, int T, const int64_t* ids, const void* weights,
+                                                 const uint64_t* expert_table_q4r, int H, int E, int I, int k,
+                                                 void* out, void* workspace, size_t ws_bytes, void* stream) {
+  return experts_forward(x, T, ids, weights, expert_table_q4r, H, E, I, k, out, workspace, ws_bytes,
+                         (hipStream_t)stream, 2);
 }
 
 // ln_w non-null: x is the hidden state h before the layer's RMSNorm; the block runs on
@@ -151,7 +158,7 @@ extern "C" int tmoe_experts_forward_int4(const void* x, int T, const int64_t* id
 static int moe_block(const void* x, int T, const void* router_w, const float* logits_in, const uint64_t* expert_table,
                      const void* sh_gate, const void* sh_up, const void* sh_down, const void* sh_gate_w, int H, int E,
                      int I, int k, int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
-                     void* workspace, size_t ws_bytes, hipStream_t s, bool q4, const void* ln_w = nullptr,
+                     void* workspace, size_t ws_bytes, hipStream_t s, int q4, const void* ln_w = nullptr,
                      float ln_eps = 0.f, uint32_t* err = nullptr) {
   const bool has_sh = sh_gate || sh_up || sh_down || sh_gate_w;
   if (has_sh && (!sh_gate || !sh_up || !sh_down || !sh_gate_w || Is < 8)) return TMOE_ERR_NULL;
@@ -230,7 +237,7 @@ extern "C" int tmoe_moe_block_bf16(const void* x, int T, const void* router_w, c
                                    void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                                    void* workspace, size_t ws_bytes, void* stream) {
   return moe_block(x, T, router_w, logits_in, expert_table, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, out,
-                   ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, false);
+                   ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, 0);
 }
 
 extern "C" int tmoe_moe_block_int4(const void* x, int T, const void* router_w, const float* logits_in,
@@ -239,7 +246,16 @@ extern "C" int tmoe_moe_block_int4(const void* x, int T, const void* router_w, c
                                    void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
                                    void* workspace, size_t ws_bytes, void* stream) {
   return moe_block(x, T, router_w, logits_in, expert_table_q4, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
-                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, true);
+                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, 1);
+}
+
+extern "C" int tmoe_moe_block_int4_f16rows(const void* x, int T, const void* router_w, const float* logits_in,
+                                           const uint64_t* expert_table_q4r, const void* sh_gate, const void* sh_up,
+                                           const void* sh_down, const void* sh_gate_w, int H, int E, int I, int k,
+                                           int Is, void* out, int64_t* ids_out, void* weights_out, uint32_t* heat,
+                                           void* workspace, size_t ws_bytes, void* stream) {
+  return moe_block(x, T, router_w, logits_in, expert_table_q4r, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
+                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, 2);
 }
 
 // The MoE sublayer of a decoder layer: out = bf16(h + block(bf16(rmsnorm(h) * (1 + ln_w)))).
@@ -250,7 +266,7 @@ extern "C" int tmoe_moe_layer_bf16(const void* h, int T, const void* ln_w, float
                                    void* workspace, size_t ws_bytes, void* stream) {
   if (!ln_w) return TMOE_ERR_NULL;
   return moe_block(h, T, router_w, logits_in, expert_table, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, out,
-                   ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, false, ln_w, eps);
+                   ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, 0, ln_w, eps);
 }
 
 extern "C" int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float eps, const void* router_w,
@@ -260,7 +276,7 @@ extern "C" int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float
                                    void* workspace, size_t ws_bytes, void* stream) {
   if (!ln_w) return TMOE_ERR_NULL;
   return moe_block(h, T, router_w, logits_in, expert_table_q4, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is,
-                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, true, ln_w, eps);
+                   out, ids_out, weights_out, heat, workspace, ws_bytes, (hipStream_t)stream, 1, ln_w, eps);
 }
 
 // ---------------------------------------------------------------- allocation-free block
@@ -308,5 +324,5 @@ extern "C" int tmoe_moe_block_bf16_noalloc(const void* x, int T, const void* rou
   void* ws = device_scratch(dev);
   if (!ws) return TMOE_ERR_HIP;
   return moe_block(x, T, router_w, logits_in, expert_table, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, out,
-                   ids_out, weights_out, heat, ws, (size_t)TMOE_STATIC_SCRATCH_BYTES, s, false, nullptr, 0.f, status);
+                   ids_out, weights_out, heat, ws, (size_t)TMOE_STATIC_SCRATCH_BYTES, s, 0, nullptr, 0.f, status);
 }

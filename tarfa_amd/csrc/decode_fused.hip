@@ -125,6 +125,11 @@ template <typename T>
 __device__ __forceinline__ T ld_inv(const T* p) {
   return *(const __attribute__((address_space(4))) T*)p;
 }
+// fp16 value idx of p (4-byte aligned), as fp32, through a wave-uniform dword load.
+__device__ __forceinline__ float ld_inv_f16(const uint16_t* p, int idx) {
+  const uint32_t w = ld_inv(reinterpret_cast<const uint32_t*>(p) + (idx >> 1));
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (w >> 16) : (w & 0xFFFFu)));
+}
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
 __device__ __forceinline__ bool has_tag(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 
@@ -272,7 +277,9 @@ __device__ __forceinline__ void down_dots(const uint16_t* w, const uint64_t* act
 // [2I, H/2], scales [2I, H/128]): fp32 gate and up values (no rounding), then
 // act = bf16(silu(g) * u) in fp32 (tarfa/engine/moe_kernel.py:100), published as R/2
 // tagged bf16 pairs.  Loads in need order: input, scales, then the 2R weight rows.
-template <int MH, int R, typename XGet, typename Take>
+// QR: the reference's own scale layout instead, one fp16 scale per row (gs [2I]): the row's
+// fp32 dot is multiplied by it once, as the reference's kernel does (moe_kernel.py:62-63).
+template <int MH, int R, bool QR, typename XGet, typename Take>
 __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int i0, int I, int H,
                                       XGet&& get_x, int lane, uint64_t* act64, uint32_t tag, Take&& take) {
   constexpr int G = 4 * MH;            // scale groups per row (H = 512 MH)
@@ -280,14 +287,24 @@ __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int
   static_assert(R % 2 == 0 && NW <= 128, "scale words of a block fit two per lane");
   XPack<MH> xf;
   get_x(xf, lane);
-  // Scale words of the R gate rows and of the R up rows: word i of a block in lane i % 64, register i / 64.
-  const uint32_t* sg = reinterpret_cast<const uint32_t*>(gs + (size_t)i0 * G);
-  const uint32_t* su = reinterpret_cast<const uint32_t*>(gs + (size_t)(I + i0) * G);
+  // Scale words of the R gate rows and of the R up rows: word i of a block in lane i % 64, register i / 64
+  // (QR: the 2R row scales, wave-uniform).
   uint32_t sc[2][2];
+  float srow[2 * R];
+  if constexpr (QR) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    sc[0][h] = (h * 64 < NW && lane + h * 64 < NW) ? sg[lane + h * 64] : 0u;
-    sc[1][h] = (h * 64 < NW && lane + h * 64 < NW) ? su[lane + h * 64] : 0u;
+    for (int r = 0; r < R; ++r) {
+      srow[r] = ld_inv_f16(gs, i0 + r);
+      srow[R + r] = ld_inv_f16(gs, I + i0 + r);
+    }
+  } else {
+    const uint32_t* sg = reinterpret_cast<const uint32_t*>(gs + (size_t)i0 * G);
+    const uint32_t* su = reinterpret_cast<const uint32_t*>(gs + (size_t)(I + i0) * G);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sc[0][h] = (h * 64 < NW && lane + h * 64 < NW) ? sg[lane + h * 64] : 0u;
+      sc[1][h] = (h * 64 < NW && lane + h * 64 < NW) ? su[lane + h * 64] : 0u;
+    }
   }
   const size_t rowb = (size_t)H / 2;
   uint32_t w[2 * R][MH];
@@ -307,11 +324,16 @@ __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int
     float a = 0.f;
 #pragma unroll
     for (int c = 0; c < MH; ++c) {
-      // Words base, base + 1 (base even: G is a multiple of 4) share one register.
-      const int base = ((r % R) * G + 4 * c) / 2;
-      a = fmaf(q4_scale(sc[r / R][base / 64], (base % 64) + (lane >> 5), sel), q4_dot8(w[r][c], qx.x[c], qx.off[c]), a);
+      if constexpr (QR) {
+        a += q4_dot8(w[r][c], qx.x[c], qx.off[c]);
+      } else {
+        // Words base, base + 1 (base even: G is a multiple of 4) share one register.
+        const int base = ((r % R) * G + 4 * c) / 2;
+        a = fmaf(q4_scale(sc[r / R][base / 64], (base % 64) + (lane >> 5), sel), q4_dot8(w[r][c], qx.x[c], qx.off[c]),
+                 a);
+      }
     }
-    v[r] = wave_sum(a);
+    v[r] = QR ? wave_sum(a) * srow[r] : wave_sum(a);
   }
   int pk[R / 2];
 #pragma unroll
@@ -328,16 +350,22 @@ __device__ __forceinline__ void up_q4(const uint8_t* gq, const uint16_t* gs, int
 // RQ rows of an int4 down projection (packed [H, I/2], scales [H, I/128]):
 // d[r] = fp32 dot(w[h0 + r], act).  Weight rows and activations are requested
 // together, as in down_dots.
-template <int MI, int RQ>
+template <int MI, int RQ, bool QR>
 __device__ __forceinline__ void down_q4(const uint8_t* dq, const uint16_t* ds, const uint64_t* act64, int I, int h0,
                                         int lane, float (&d)[RQ], uint32_t tag, uint32_t* err) {
   constexpr int G = 4 * MI;            // scale groups per row (I = 512 MI)
   constexpr int NW = RQ * G / 2;       // scale words of the RQ rows
   static_assert(NW <= 128, "scale words fit two per lane");
-  const uint32_t* sp = reinterpret_cast<const uint32_t*>(ds + (size_t)h0 * G);
   uint32_t sc[2];
+  float srow[RQ];
+  if constexpr (QR) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) sc[h] = (h * 64 < NW && lane + h * 64 < NW) ? sp[lane + h * 64] : 0u;
+    for (int r = 0; r < RQ; ++r) srow[r] = ld_inv_f16(ds, h0 + r);
+  } else {
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(ds + (size_t)h0 * G);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sc[h] = (h * 64 < NW && lane + h * 64 < NW) ? sp[lane + h * 64] : 0u;
+  }
   const size_t rowb = (size_t)I / 2;
   uint32_t w[RQ][MI];
 #pragma unroll
@@ -354,10 +382,14 @@ __device__ __forceinline__ void down_q4(const uint8_t* dq, const uint16_t* ds, c
     float a = 0.f;
 #pragma unroll
     for (int c = 0; c < MI; ++c) {
-      const int base = (r * G + 4 * c) / 2;   // even: words base, base + 1 share one register
-      a = fmaf(q4_scale(sc[base / 64], (base % 64) + (lane >> 5), sel), q4_dot8(w[r][c], qa.x[c], qa.off[c]), a);
+      if constexpr (QR) {
+        a += q4_dot8(w[r][c], qa.x[c], qa.off[c]);
+      } else {
+        const int base = (r * G + 4 * c) / 2;   // even: words base, base + 1 share one register
+        a = fmaf(q4_scale(sc[base / 64], (base % 64) + (lane >> 5), sel), q4_dot8(w[r][c], qa.x[c], qa.off[c]), a);
+      }
     }
-    d[r] = wave_sum(a);
+    d[r] = QR ? wave_sum(a) * srow[r] : wave_sum(a);
   }
 }
 
@@ -714,7 +746,7 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
 
 // Int4 mode, a D task of routed slot j: RQ rows published as one fp32 word each (a
 // skipped slot publishes zeros the combine ignores), or combined for the last slot.
-template <int MI, int RQ, typename Take>
+template <int MI, int RQ, bool QR, typename Take>
 __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, int idx, int lane, uint32_t& rwc,
                                              uint32_t tag, uint32_t* err, RouteLds& L, Take&& take) {
   const int e = wave_slot_expert(p, slot, rwc);
@@ -723,7 +755,7 @@ __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, in
 #pragma unroll
   for (int r = 0; r < RQ; ++r) d[r] = 0.f;
   if (e >= 0)
-    down_q4<MI, RQ>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
+    down_q4<MI, RQ, QR>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 3)), p.act64 + (size_t)slot * p.I / 2,
                     p.I, h0, lane, d, tag, err);
   if (e >= 0) take();
@@ -793,8 +825,9 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
 // none of that code is in the kernel.
 // TRACE: the debug-timeline instantiation (exact-fit block shapes only); without it the
 // pointer is a null constant and no recording code or state is in the kernel.
-template <int MH, int MI, bool EXACT, bool Q4, bool LN, bool TRACE = false>
+template <int MH, int MI, bool EXACT, bool Q4, bool LN, bool TRACE = false, bool QR = false>
 __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
+  static_assert(!QR || Q4, "per-row scales are an int4 format");
   static_assert(!Q4 || EXACT, "int4 variants need H and I multiples of 512");
   if constexpr (!LN) {
     p.ln_w = nullptr;
@@ -926,7 +959,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       const int n_rows = shared ? p.Is : p.I;
       if (Q4 && !shared) {
         if (e >= 0)
-          up_q4<MH, kQ4Pairs>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
+          up_q4<MH, kQ4Pairs, QR>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 1)), tk.idx * kQ4Pairs, p.I, p.H,
                     get_x, lane, p.act64 + (size_t)tk.slot * p.I / 2, tag, take);
       } else if (e >= 0) {
@@ -938,7 +971,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
                             p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2), tag, take);
       }
     } else if (Q4 && tk.type == kTD) {
-      task_down_q4<MI, RQ>(p, tk.slot, tk.idx, lane, rwc, tag, err, s_rt, take);
+      task_down_q4<MI, RQ, QR>(p, tk.slot, tk.idx, lane, rwc, tag, err, s_rt, take);
     } else {
       // Down rows: the shared expert (SD) or routed slot j (D); D(k-1) combines.
       const bool shared = tk.type == kTSD;
@@ -1016,9 +1049,21 @@ typedef void (*FusedKernel)(DecodeParams);
 // masked variants cover the rest up to H = 4096, I = Is = 2048.
 // Int4 mode has exact-fit variants only.
 template <bool LN>
-static FusedKernel pick_fused_t(int H, int I, int Is, bool q4) {
+static FusedKernel pick_fused_t(int H, int I, int Is, bool q4, bool qr) {
   if (H % 512 == 0 && I % 512 == 0 && (Is == 0 || Is == I)) {
     const int key = (H / 512) * 10 + I / 512;
+    if (qr) {   // int4 with the reference's per-row fp16 scales
+      switch (key) {
+        case 11: return k_decode_fused<1, 1, true, true, LN, false, true>;
+        case 21: return k_decode_fused<2, 1, true, true, LN, false, true>;
+        case 22: return k_decode_fused<2, 2, true, true, LN, false, true>;
+        case 42: return k_decode_fused<4, 2, true, true, LN, false, true>;
+        case 52: return k_decode_fused<5, 2, true, true, LN, false, true>;
+        case 62: return k_decode_fused<6, 2, true, true, LN, false, true>;
+        case 84: return k_decode_fused<8, 4, true, true, LN, false, true>;
+      }
+      return nullptr;
+    }
     if (q4) {
       switch (key) {
         case 11: return k_decode_fused<1, 1, true, true, LN>;
@@ -1040,7 +1085,7 @@ static FusedKernel pick_fused_t(int H, int I, int Is, bool q4) {
       case 84: return k_decode_fused<8, 4, true, false, LN>;
     }
   }
-  if (q4) return nullptr;
+  if (q4 || qr) return nullptr;
   const int inter = I > Is ? I : Is;
   const int ncH = (H + 511) / 512, ncI = (inter + 511) / 512;
   const int mh = ncH <= 2 ? 2 : ncH <= 4 ? 4 : ncH <= 6 ? 6 : ncH <= 8 ? 8 : 0;
@@ -1057,12 +1102,13 @@ static FusedKernel pick_fused_t(int H, int I, int Is, bool q4) {
   }
   return nullptr;
 }
-static FusedKernel pick_fused(int H, int I, int Is, bool q4, bool ln) {
-  return ln ? pick_fused_t<true>(H, I, Is, q4) : pick_fused_t<false>(H, I, Is, q4);
+// q4: 0 bf16 experts, 1 int4 with group-128 bf16 scales, 2 int4 with per-row fp16 scales.
+static FusedKernel pick_fused(int H, int I, int Is, int q4, bool ln) {
+  return ln ? pick_fused_t<true>(H, I, Is, q4 != 0, q4 == 2) : pick_fused_t<false>(H, I, Is, q4 != 0, q4 == 2);
 }
 // The recording twin of a block-mode exact-fit kernel, or null.
-static FusedKernel pick_traced(int H, int I, int Is, bool q4, bool ln) {
-  if (ln || H % 512 || I % 512 || (Is != 0 && Is != I)) return nullptr;
+static FusedKernel pick_traced(int H, int I, int Is, int q4, bool ln) {
+  if (ln || q4 == 2 || H % 512 || I % 512 || (Is != 0 && Is != I)) return nullptr;
   switch ((H / 512) * 10 + I / 512) {
     case 11: return q4 ? k_decode_fused<1, 1, true, true, false, true> : nullptr;
     case 21: return q4 ? k_decode_fused<2, 1, true, true, false, true> : k_decode_fused<2, 1, true, false, false, true>;
@@ -1106,7 +1152,7 @@ static size_t g_trace_bytes = 0;
 
 int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   const bool has_sh = p.sh_gate != nullptr;
-  FusedKernel k = pick_fused(p.H, p.I, p.Is, p.q4 != 0, p.ln_w != nullptr);
+  FusedKernel k = pick_fused(p.H, p.I, p.Is, p.q4, p.ln_w != nullptr);
   if (!k || p.k > kFusedMaxK || (has_sh && !run_router) || (p.I & 1) || (p.Is & 1) || (p.H % kDownRows))
     return TMOE_ERR_SHAPE;
   const int n_rows = (p.logits_in ? 0 : p.E) + (has_sh ? 1 : 0);
@@ -1136,7 +1182,7 @@ int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
     p.trace = g_trace && trace_words(p.n_tasks, grid * kWaves) * 8 <= g_trace_bytes ? g_trace : nullptr;
   }
   if (p.trace) {
-    FusedKernel kt = pick_traced(p.H, p.I, p.Is, p.q4 != 0, p.ln_w != nullptr);
+    FusedKernel kt = pick_traced(p.H, p.I, p.Is, p.q4, p.ln_w != nullptr);
     if (kt && resident_blocks(kt) >= grid) k = kt;
     else p.trace = nullptr;
   }

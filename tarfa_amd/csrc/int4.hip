@@ -1,4 +1,5 @@
-// Int4 fast-mode weight format: quantise and dequantise (debug materialisation).
+// Int4 fast-mode weight format: quantise and dequantise (debug materialisation), and the
+// reference's own fp16 dequantisation of its per-row-scale files.
 //
 // Format (a group-scaled form of the reference's per-row int4 layout,
 // tarfa/engine/channel_q4.py:10-14, tarfa/engine/moe_kernel.py:110-114):
@@ -67,6 +68,35 @@ __global__ __launch_bounds__(256) void k_dequant_int4(const uint8_t* __restrict_
   }
 }
 
+// The reference's own dequantisation (tarfa/engine/channel_q4.py:10-14,
+// moe_kernel.py:110-114): fp16 scales, fp16 result, w = fp16((nibble - 8) * s[n, k / G]).
+// The product of a 4-bit integer and an 11-bit fp16 significand is exact in fp32, so one
+// round-to-nearest-even conversion to fp16 (subnormals kept) gives torch's fp16 multiply.
+// With G = K the scale is per row, the reference's layout.
+__global__ __launch_bounds__(256) void k_dequant_int4_f16(const uint8_t* __restrict__ packed,
+                                                          const uint16_t* __restrict__ scales, int N, int K, int G,
+                                                          uint16_t* __restrict__ out) {
+  const size_t total = (size_t)N * K / 8;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const size_t e0 = u * 8;
+    const int n = (int)(e0 / K), k0 = (int)(e0 % K);
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(packed + (size_t)n * (K / 2) + k0 / 2);
+    uint16_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int q = (int)((word >> (4 * j)) & 0xFu) - 8;
+      const float s = (float)__builtin_bit_cast(_Float16, scales[(size_t)n * (K / G) + (k0 + j) / G]);
+      v[j] = __builtin_bit_cast(uint16_t, (_Float16)((float)q * s));
+    }
+    u32x4 pk;
+    pk.x = v[0] | ((uint32_t)v[1] << 16);
+    pk.y = v[2] | ((uint32_t)v[3] << 16);
+    pk.z = v[4] | ((uint32_t)v[5] << 16);
+    pk.w = v[6] | ((uint32_t)v[7] << 16);
+    *reinterpret_cast<u32x4*>(out + e0) = pk;
+  }
+}
+
 }  // namespace tmoe
 
 using namespace tmoe;
@@ -95,6 +125,18 @@ extern "C" int tmoe_dequant_int4_bf16(const void* packed, const void* scales, in
   const size_t units = (size_t)N * K / 8;
   const int blocks = (int)((units + 255) / 256 < 4096 ? (units + 255) / 256 : 4096);
   hipLaunchKernelGGL(k_dequant_int4, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)packed,
+                     (const uint16_t*)scales, N, K, G, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+}
+
+extern "C" int tmoe_dequant_int4_f16(const void* packed, const void* scales, int N, int K, int G, void* out,
+                                     void* stream) {
+  if (!packed || !out || !scales) return TMOE_ERR_NULL;
+  if (N < 1 || K < 8 || K % 8 || G < 2 || G % 2 || K % G) return TMOE_ERR_SHAPE;
+  if (((uintptr_t)packed & 3u) || ((uintptr_t)out & 15u)) return TMOE_ERR_ALIGN;
+  const size_t units = (size_t)N * K / 8;
+  const int blocks = (int)((units + 255) / 256 < 4096 ? (units + 255) / 256 : 4096);
+  hipLaunchKernelGGL(k_dequant_int4_f16, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)packed,
                      (const uint16_t*)scales, N, K, G, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }

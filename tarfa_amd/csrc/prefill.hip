@@ -219,6 +219,12 @@ __device__ __forceinline__ u32x4 dequant_frag(uint32_t w, float s) {
   }
   return u32x4{d[0], d[1], d[2], d[3]};
 }
+// A scale's 16 bits as fp32: bf16 (group scales) or fp16 (QR, per-row scales).
+template <bool QR>
+__device__ __forceinline__ float scale_f32(uint16_t b) {
+  if constexpr (QR) return (float)__builtin_bit_cast(_Float16, b);
+  else return bf16_to_f32(b);
+}
 
 // Block = 4 waves; tile = (up to 256 rows of one group) x (two 16-row weight sets per
 // wave).  A is staged through LDS (double-buffered, one barrier per 64-wide K stage);
@@ -230,7 +236,9 @@ __device__ __forceinline__ u32x4 dequant_frag(uint32_t w, float s) {
 // RING = K stages requested ahead of the multiply; Q4: routed weights are int4 (table
 // [E][4]), dequantised into the B fragments in registers (a launch covers either the
 // routed groups in int4 or the shared group in bf16, never both).
-template <int RING, bool Q4>
+// QR (with Q4): the reference's scale layout, one fp16 scale per weight row; the weight is
+// then bf16((n - 8) * s) with s that row's scale (the product is exact in fp32).
+template <int RING, bool Q4, bool QR = false>
 __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][kBM * kLdsStride];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -281,8 +289,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
     const int row = lane & 15;
     q0 = pk + (size_t)(r0w + row) * (K / 2) + 4 * (lane >> 4);
     q1 = pk + (size_t)(r1w + row) * (K / 2) + 4 * (lane >> 4);
-    s0 = sc + (size_t)(r0w + row) * (K / 128);
-    s1 = sc + (size_t)(r1w + row) * (K / 128);
+    s0 = sc + (size_t)(r0w + row) * (QR ? 1 : K / 128);
+    s1 = sc + (size_t)(r1w + row) * (QR ? 1 : K / 128);
   } else {
     const uint16_t *w0, *w1;
     if (p.up) {
@@ -343,8 +351,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
         qreg[slot][ks][0] = *(const __attribute__((address_space(1))) uint32_t*)(q0 + (k0 + 32 * ks) / 2);
         qreg[slot][ks][1] = *(const __attribute__((address_space(1))) uint32_t*)(q1 + (k0 + 32 * ks) / 2);
       }
-      sreg[slot][0] = s0[k0 / 128];
-      sreg[slot][1] = s1[k0 / 128];
+      sreg[slot][0] = s0[QR ? 0 : k0 / 128];
+      sreg[slot][1] = s1[QR ? 0 : k0 / 128];
     } else {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -368,8 +376,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GemmParams p) {
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8_t bg, bu;
       if constexpr (Q4) {
-        bg = as_bf16x8(dequant_frag(qreg[slot][ks][0], bf16_to_f32((uint16_t)sreg[slot][0])));
-        bu = as_bf16x8(dequant_frag(qreg[slot][ks][1], bf16_to_f32((uint16_t)sreg[slot][1])));
+        bg = as_bf16x8(dequant_frag(qreg[slot][ks][0], scale_f32<QR>((uint16_t)sreg[slot][0])));
+        bu = as_bf16x8(dequant_frag(qreg[slot][ks][1], scale_f32<QR>((uint16_t)sreg[slot][1])));
       } else {
         bg = as_bf16x8(breg[slot][ks][0]);
         bu = as_bf16x8(breg[slot][ks][1]);
@@ -525,6 +533,11 @@ __device__ __forceinline__ uint32_t gld4(const void* sbase, uint32_t voff) {
   asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
   return v;
 }
+__device__ __forceinline__ uint32_t gld2(const void* sbase, uint32_t voff) {
+  uint32_t v;
+  asm volatile("global_load_ushort %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
+  return v;
+}
 // 16 bytes per lane from global memory straight into LDS at lds + 16 lane (M0 = lds).
 // Nothing else in the kernel uses M0.
 __device__ __forceinline__ void gdma16(const void* sbase, uint32_t voff, const void* lds) {
@@ -543,7 +556,7 @@ struct PTile {
   int m;                    // valid rows
 };
 
-template <bool Q4>
+template <bool Q4, bool QR = false>
 __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   __shared__ u32x4 lA0[kPSlot], lA1[kPSlot], lA2[kPSlot], lA3[kPSlot], lA4[kPSlot], lA5[kPSlot], lA6[kPSlot],
       lA7[kPSlot];
@@ -589,7 +602,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
       for (int nb = 0; nb < kPNB; ++nb) {
         const int wr = p.up ? (nb ? p.I : 0) + c0 : c0 + 16 * nb;
         t.q[nb] = pk + (size_t)wr * (K / 2);
-        t.sc[nb] = sc + (size_t)wr * (K / 128);
+        t.sc[nb] = sc + (size_t)wr * (QR ? 1 : K / 128);
         t.b[nb] = nullptr;
       }
     } else {
@@ -645,7 +658,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   // the last row) and are kept for the current and the next tile.
   const uint32_t b_off = (uint32_t)((lrow * K + lk) * 2);
   const uint32_t q_off = (uint32_t)(lrow * (K / 2) + lk / 2);
-  const uint32_t s_off = (uint32_t)(lrow * (K / 128) * 2);
+  const uint32_t s_off = (uint32_t)(lrow * (QR ? 1 : K / 128) * 2);
   // A rows: up: x[perm[arow0 + r] / k] (routed) or x[arow0 + r] (shared); down:
   // act[arow0 + r].  Rows past the tile's count repeat its last row.  The perm entries of
   // a tile are fetched (pipeline loads, not counted by the compiler) a whole tile before
@@ -687,8 +700,10 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
         qreg[slot][nb][0] = gld4(qr, q_off);
         qreg[slot][nb][1] = gld4(qr + 16, q_off);
         // The 32-bit word holding this stage's scale (table entries are 16-byte aligned
-        // and K / 128 is even here); multiply() takes its half.
-        sreg[slot][nb] = gld4(gaddr(nx ? nxt.sc[nb] : cur.sc[nb], (size_t)((k0 / 128) & ~1) * 2), s_off);
+        // and K / 128 is even here); multiply() takes its half.  QR: the row's one fp16
+        // scale, reloaded each stage so the stage's load count stays the same.
+        if constexpr (QR) sreg[slot][nb] = gld2(gaddr(nx ? nxt.sc[nb] : cur.sc[nb], 0), s_off);
+        else sreg[slot][nb] = gld4(gaddr(nx ? nxt.sc[nb] : cur.sc[nb], (size_t)((k0 / 128) & ~1) * 2), s_off);
       } else {
         const char* br = gaddr(nx ? nxt.b[nb] : cur.b[nb], (size_t)k0 * 2);
         breg[slot][nb][0] = gld16(br, b_off);
@@ -726,7 +741,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
         if constexpr (Q4) {
           const uint32_t sr = sreg[bs][nb];
           const uint32_t bits = ((u >> 1) & 1) ? (sr & 0xFFFF0000u) : (sr << 16);
-          b[nb] = as_bf16x8(dequant_frag(qreg[bs][nb][ks], __uint_as_float(bits)));
+          b[nb] = as_bf16x8(dequant_frag(qreg[bs][nb][ks], QR ? scale_f32<true>((uint16_t)sr) : __uint_as_float(bits)));
         } else {
           b[nb] = as_bf16x8(breg[bs][nb][ks]);
         }
@@ -966,8 +981,10 @@ int dispatch_launch(const int32_t* ids32, const int64_t* ids64, int T, int k, in
 int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
-                   void* ws, hipStream_t s, bool q4, const uint16_t* resid, uint32_t* err) {
+                   void* ws, hipStream_t s, int q4, const uint16_t* resid, uint32_t* err) {
+  // q4: 0 bf16 experts, 1 int4 with group-128 bf16 scales, 2 int4 with per-row fp16 scales.
   const bool has_sh = sh_gate != nullptr;
+  const bool qr = q4 == 2;
   if (H % 128 || I % 64 || E > 1023 || (has_sh && Is != I)) return TMOE_ERR_SHAPE;
   if (q4 && I % 128) return TMOE_ERR_SHAPE;   // int4: every 64-wide K stage inside one 128-column group
   const Ws L = ws_layout(T, H, E, I, k, Is);
@@ -1008,10 +1025,14 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
     g.group_lo = lo;
     g.group_hi = hi;
     const long grid = (mchunks * g.n_ntiles + 7) / 8 * 8;
-    if (persistent && routed_q4)
+    if (persistent && routed_q4 && qr)
+      hipLaunchKernelGGL((k_grouped_gemm_p<true, true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (persistent && routed_q4)
       hipLaunchKernelGGL((k_grouped_gemm_p<true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent)
       hipLaunchKernelGGL((k_grouped_gemm_p<false>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (routed_q4 && qr)
+      hipLaunchKernelGGL((k_grouped_gemm<kRing, true, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
     else if (routed_q4)
       hipLaunchKernelGGL((k_grouped_gemm<kRing, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
     else

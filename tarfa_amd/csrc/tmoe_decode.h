@@ -13,7 +13,7 @@ struct DecodeParams {
   const uint16_t* router_w;   // [E, H] or null (logits supplied or experts-only mode)
   const float* logits_in;     // [E] or null
   const uint64_t* table;      // [E][2] gate_up / down base pointers; int4: [E][4] (packed, scales) x 2
-  int q4;                     // 1: int4 routed experts (group-128 bf16 scales), fp32 combine
+  int q4;                     // int4 routed experts, fp32 combine: 1 group-128 bf16 scales, 2 per-row fp16 scales
   const uint16_t* sh_gate;    // [Is, H]   (null = no shared expert)
   const uint16_t* sh_up;      // [Is, H]
   const uint16_t* sh_down;    // [H, Is]

@@ -33,7 +33,8 @@ import weakref
 import torch
 
 from ._lib import check
-from .moe import MoEShape, Workspace, expert_table, expert_table_q4, experts_forward, moe_block
+from .int4_files import Int4LayerFile
+from .moe import MoEShape, Workspace, expert_table, expert_table_q4, expert_table_q4_rows, experts_forward, moe_block
 from .residency import RouteTelemetry
 
 ENGINE_DTYPE = torch.bfloat16
@@ -187,6 +188,22 @@ class ExpertStore:
         """Int4 experts (labelled fast mode): packed [E,2I,H/2] / [E,H,I/2] u8, group scales bf16."""
         ts = (gate_up_q, gate_up_s, down_q, down_s)
         return cls(shape, expert_table_q4(*ts), gate_up_q.device, keepalive=ts, **book)
+
+    @classmethod
+    def from_int4_rows(cls, shape, gate_up_q, gate_up_s, down_q, down_s, **book):
+        """Int4 experts in the reference's own layout: packed as above, ONE fp16 scale per
+        row (gate_up_s [E,2I], down_s [E,H]; tarfa/engine/channel_q4.py:10-14)."""
+        ts = (gate_up_q, gate_up_s, down_q, down_s)
+        return cls(shape, expert_table_q4_rows(*ts), gate_up_q.device, keepalive=ts, **book)
+
+    @classmethod
+    def from_int4_file(cls, shape, path, device, **book):
+        """One layer file of the reference's int4 experts (channel_q4.py:18, 28-38), all of
+        its experts loaded into HBM."""
+        f = Int4LayerFile(path)
+        if (f.hidden, f.intermediate, f.num_experts) != (shape.hidden, shape.intermediate, shape.num_experts):
+            raise ValueError(f"{path}: H={f.hidden} I={f.intermediate} E={f.num_experts} does not match {shape}")
+        return cls.from_int4_rows(shape, *f.load(device), **book)
 
     @property
     def int4(self):

@@ -98,6 +98,50 @@ def expert_table_q4(gate_up_q, gate_up_s, down_q, down_s):
     return host.to(gate_up_q.device)
 
 
+class Int4RowTable:
+    """[E, 4] device table of int4 experts in the reference's own layout: packed rows with
+    ONE fp16 scale per row (tarfa/engine/channel_q4.py:10-14, 18, 28-38)."""
+
+    def __init__(self, table):
+        self.table = table
+
+    @property
+    def shape(self):
+        return self.table.shape
+
+    def data_ptr(self):
+        return self.table.data_ptr()
+
+
+def expert_table_q4_rows(gate_up_q, gate_up_s, down_q, down_s):
+    """Int4RowTable for packed gate_up [E,2I,H/2] u8, its scales [E,2I] fp16, packed down
+    [E,H,I/2] u8, its scales [E,H] fp16."""
+    for name, t, dt in (("gate_up_q", gate_up_q, torch.uint8), ("gate_up_s", gate_up_s, torch.float16),
+                        ("down_q", down_q, torch.uint8), ("down_s", down_s, torch.float16)):
+        if t.dtype != dt:
+            raise TypeError(f"{name} must be {dt}, got {t.dtype}")
+    if gate_up_s.dim() != 2 or down_s.dim() != 2:
+        raise ValueError("per-row scales are [E, rows]")
+    return Int4RowTable(expert_table_q4(gate_up_q, gate_up_s, down_q, down_s))
+
+
+def dequant_int4_f16(packed, scales, group=None):
+    """The reference's dequant_int4 (channel_q4.py:10-14) on the device: packed [..., K/2]
+    uint8 and fp16 scales [..., K/group] (group = K, the default: one scale per row) ->
+    fp16 [..., K] = fp16((nibble - 8) * scale), bit for bit."""
+    _need(packed, "packed", torch.uint8)
+    _need(scales, "scales", torch.float16, None, packed.device)
+    K = packed.shape[-1] * 2
+    N = packed.numel() * 2 // K
+    group = K if group is None else group
+    if scales.numel() != N * (K // group):
+        raise ValueError("scales do not match packed and group")
+    out = torch.empty(*packed.shape[:-1], K, dtype=torch.float16, device=packed.device)
+    check(lib().tmoe_dequant_int4_f16(_p(packed), _p(scales), N, K, group, _p(out), _stream(packed.device)),
+          "tmoe_dequant_int4_f16")
+    return out
+
+
 def quantize_int4(w, group=128):
     """bf16 [..., K] -> (packed [..., K/2] uint8, scales [..., K/group] bf16) on the device."""
     _need(w, "w", torch.bfloat16)
@@ -125,11 +169,17 @@ def dequant_int4(packed, scales, group=128):
 
 
 def _table_kind(table, E, dev):
-    """2 columns: bf16 experts; 4 columns: int4 experts."""
-    _need(table, "expert_table", torch.int64, None, dev)
-    if table.dim() != 2 or table.shape[0] != E or table.shape[1] not in (2, 4):
-        raise ValueError(f"expert_table must be [E, 2] (bf16) or [E, 4] (int4), got {tuple(table.shape)}")
-    return table.shape[1] == 4
+    """0: bf16 experts ([E, 2]); 1: int4 with group scales ([E, 4]); 2: int4 in the
+    reference's per-row fp16 layout (Int4RowTable)."""
+    rows = isinstance(table, Int4RowTable)
+    t = table.table if rows else table
+    _need(t, "expert_table", torch.int64, None, dev)
+    if t.dim() != 2 or t.shape[0] != E or t.shape[1] not in (2, 4) or (rows and t.shape[1] != 4):
+        raise ValueError(f"expert_table must be [E, 2] (bf16) or [E, 4] (int4), got {tuple(t.shape)}")
+    return 2 if rows else (1 if t.shape[1] == 4 else 0)
+
+
+_INT4_SUFFIX = {0: "bf16", 1: "int4", 2: "int4_f16rows"}
 
 
 def router_topk(shape: MoEShape, x=None, router_w=None, logits=None, heat=None):
@@ -173,7 +223,8 @@ def dispatch(ids, num_experts, workspace: Workspace):
 def experts_forward(shape: MoEShape, x, ids, weights, table, workspace: Workspace, out=None):
     """Routed experts only (the reference's experts.forward); returns out [T,H] bf16.
 
-    ``table`` [E, 2] selects exact bf16 experts, [E, 4] (expert_table_q4) the int4 fast mode.
+    ``table`` [E, 2] selects exact bf16 experts, [E, 4] (expert_table_q4) the int4 fast mode,
+    an Int4RowTable (expert_table_q4_rows) the reference's own per-row fp16 int4 layout.
     """
     H, E, I, k = shape.hidden, shape.num_experts, shape.intermediate, shape.top_k
     _need(x, "hidden_states", torch.bfloat16)
@@ -185,7 +236,7 @@ def experts_forward(shape: MoEShape, x, ids, weights, table, workspace: Workspac
     if out is None:
         out = torch.empty_like(x)
     buf = workspace.ensure(T)
-    fn = "tmoe_experts_forward_int4" if q4 else "tmoe_experts_forward_bf16"
+    fn = "tmoe_experts_forward_" + _INT4_SUFFIX[q4]
     st = getattr(lib(), fn)(_p(x), T, _p(ids), _p(weights), _p(table), H, E, I, k, _p(out), _p(buf), buf.numel(),
                             _stream(dev))
     check(st, fn)
@@ -234,7 +285,9 @@ def moe_block(shape: MoEShape, x, table, workspace: Workspace, router_w=None, lo
     weights = torch.empty(T, k, dtype=torch.bfloat16, device=dev) if weights is None else weights
     buf = workspace.ensure(T)
     ln = [] if _ln is None else [_p(_ln[0]), _ln[1]]
-    fn = ("tmoe_moe_layer_" if _ln is not None else "tmoe_moe_block_") + ("int4" if q4 else "bf16")
+    if _ln is not None and q4 == 2:
+        raise ValueError("the sublayer entry points take bf16 or group-scaled int4 experts")
+    fn = ("tmoe_moe_layer_" if _ln is not None else "tmoe_moe_block_") + _INT4_SUFFIX[q4]
     st = getattr(lib(), fn)(_p(x), T, *ln, _p(router_w) if logits is None else None, _p(logits), _p(table),
                             *[_p(t) for t in sh], H, E, I, k, Is if shared is not None else 0, _p(out),
                             _p(ids), _p(weights), _p(heat), _p(buf), buf.numel(), _stream(dev))

@@ -506,3 +506,85 @@ def test_zipf_logits_follow_the_rank_weights():
         sel[l].scatter_add_(0, lg[:, l].topk(4, -1).indices.reshape(-1), torch.ones(T * 4))
         by_rank = sel[l][torch.argsort(ranks[l])]
         assert by_rank[0] > by_rank[4] > by_rank[16] > by_rank[31]
+
+
+# ------------------------------------------------------------------ int4, the reference's per-row fp16 layout
+
+def test_dequant_f16_exhaustive_codes_times_all_fp16_scales():
+    """16 codes x every finite fp16 scale vs channel_q4.py:10-14 run in torch CPU fp16."""
+    sb = np.arange(1 << 16, dtype=np.uint16)
+    sb = sb[np.isfinite(sb.view(np.float16))]
+    packed = (np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4))[None, :]
+    packed = np.repeat(packed, sb.size, axis=0)                 # [n, 16] -> K = 32, one scale per row
+    got = int4.dequant_f16(packed, sb[:, None], group=32)
+    p = torch.from_numpy(packed)
+    lo = (p & 0xF).to(torch.int16) - 8
+    hi = ((p >> 4) & 0xF).to(torch.int16) - 8
+    q = torch.stack([lo, hi], dim=-1).reshape(p.shape[0], -1)
+    scale = torch.from_numpy(sb.view(np.int16)).view(torch.float16)
+    want = (q.to(torch.float16) * scale[:, None]).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _ref_ffn_fp16_rows(x, gup, gus, dp, ds, rw):
+    """The reference's _ref_ffn (moe_kernel.py:117-125): fp16 dequant (channel_q4.py:10-14)
+    with per-row fp16 scales, .float(), fp32 matmuls, written as the reference writes it."""
+    out = torch.zeros(x.shape[0], dtype=torch.float32)
+    xf = torch.from_numpy(np.asarray(x, np.float32))
+    for e in range(gup.shape[0]):
+        def deq(pk, sc):
+            p = torch.from_numpy(pk)
+            lo = (p & 0xF).to(torch.int16) - 8
+            hi = ((p >> 4) & 0xF).to(torch.int16) - 8
+            q = torch.stack([lo, hi], dim=-1).reshape(p.shape[0], -1)
+            return q.to(torch.float16) * torch.from_numpy(sc.view(np.int16)).view(torch.float16)[:, None]
+        gw, dw = deq(gup[e], gus[e]).float(), deq(dp[e], ds[e]).float()
+        gu = gw @ xf
+        g, u = gu.chunk(2)
+        a = F.silu(g) * u
+        out += float(rw[e]) * (dw @ a)
+    return out.numpy()
+
+
+def test_int4_ffn_rows_against_reference_ref_ffn():
+    """ffn_rows vs the reference's own closed form on its per-row fp16 layout (random packed
+    weights, fp16 scales ~N(0, 0.02), x ~ 0.5 N(0, 1): the data of moe_kernel.py:128-139);
+    the reference's criterion max|err| / max|ref| < 2e-2 and a tighter rel-L2."""
+    g = np.random.default_rng(7)
+    E, H, I = 4, 512, 256
+    gup = g.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    dp = g.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    gus = (g.standard_normal((E, 2 * I)) * 0.02).astype(np.float16).view(np.uint16)
+    ds = (g.standard_normal((E, H)) * 0.02).astype(np.float16).view(np.uint16)
+    x = bf16.rnd(g.standard_normal(H).astype(np.float32) * 0.5)
+    rw = bf16.rnd(torch.softmax(torch.from_numpy(g.standard_normal(E).astype(np.float32)), 0).numpy())
+    ref = _ref_ffn_fp16_rows(x, gup, gus, dp, ds, rw)
+    got = int4.ffn_rows(x, [(gup[e], gus[e], dp[e], ds[e]) for e in range(E)], rw)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 2e-2
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2   # the reference's bf16 act rounding aside
+
+
+def test_int4_gemv_rows_brute_force():
+    """gemv_rows against a plain double loop on a 3 x 64 case with distinct row scales."""
+    g = np.random.default_rng(11)
+    pk = g.integers(0, 256, (3, 32), dtype=np.uint8)
+    sc = np.array([0.5, -0.0625, 3.0], np.float16).view(np.uint16)
+    x = g.standard_normal(64).astype(np.float32)
+    got = int4.gemv_rows(pk, sc, x)
+    for n in range(3):
+        acc = 0.0
+        for b in range(32):
+            acc += ((int(pk[n, b]) & 0xF) - 8) * float(x[2 * b]) + ((int(pk[n, b]) >> 4) - 8) * float(x[2 * b + 1])
+        want = np.float32(np.float32(acc) * np.float32(np.array(sc[n], np.uint16).view(np.float16)))
+        assert got[n] == want
+
+
+def test_int4_dequant_rows_bf16_matches_torch():
+    g = np.random.default_rng(12)
+    pk = g.integers(0, 256, (64, 64), dtype=np.uint8)
+    sc = (g.standard_normal(64) * 0.02).astype(np.float16).view(np.uint16)
+    got = int4.dequant_rows_bf16(pk, sc)
+    q = torch.from_numpy(int4.codes(pk)).float()
+    s = torch.from_numpy(sc.view(np.int16)).view(torch.float16).float()[:, None]
+    want = (q * s).to(BF).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
