@@ -22,6 +22,9 @@ compute stream, so no queued kernel reads a slot being overwritten), then
 switches their table rows; ``table(layer)`` makes the compute stream wait on that
 stream's event before the layer's next call.
 
+``load_jnf`` fills either mode from the reference's on-disk format (JNF v1, verified by
+SHA-256 as it is read; tarfa_amd.jnf).
+
 Heat: the fused router kernel adds 1 to heat[l, e] for every selection (device
 atomics, no host sync).  ``hotlist`` turns a heat snapshot into the reference's
 hotlist fields (per-layer counts and predicted coverage for 1, 2, 4, 8 slots).
@@ -167,6 +170,63 @@ class ResidencyLedger:
         """Copy a layer's experts from full tensors ([E, ...] per part, any device)."""
         self._store(layer, 0, [p.to(self.device) if not self.tiered else p for p in parts])
         torch.cuda.synchronize(self.device)
+
+    def load_jnf(self, jnf, layers=None, verify=True, chunk=16):
+        """Fill the ledger from a JNF v1 tree (``tarfa_amd.jnf.JnfModel``); layer l of the ledger
+        takes JNF layer ``layers[l]`` (default: the same index).  Every expert's SHA-256 is
+        checked as it is read (``verify``).
+
+        Resident mode: experts go through two pinned staging buffers of ``chunk`` experts --
+        while one buffer's copy to HBM runs on the side stream, the next chunk is read into the
+        other (the reference's read_bf16 path, exact_bf16.py:163-193, with the copy overlapped).
+        Tiered mode: the file is read straight into the pinned host tier the kernels read
+        non-resident experts from; the experts already assigned HBM slots are then copied in on
+        the side stream, and ``table(layer)`` orders the next call after them."""
+        if self.int4:
+            raise ValueError("JNF holds bf16 experts; fill an int4 ledger from a bf16 one (quantized_from)")
+        E, dev = self.shape.num_experts, self.device
+        src = list(range(self.L)) if layers is None else [int(l) for l in layers]
+        if len(src) != self.L:
+            raise ValueError(f"{len(src)} JNF layers for a ledger of {self.L}")
+        for l, jl in enumerate(src):
+            ly = jnf.layers.get(jl)
+            if ly is None or (ly.num_experts, ly.hidden, ly.intermediate) != (E, self.shape.hidden,
+                                                                             self.shape.intermediate):
+                raise ValueError(f"JNF layer {jl} missing or not of shape {self.shape}")
+        side = self._side_stream()
+        side.wait_stream(torch.cuda.current_stream(dev))
+        if self.tiered:
+            for l, jl in enumerate(src):
+                jnf.read_experts(jl, range(E), self.host[l][0], self.host[l][1], verify=verify)
+                with torch.cuda.stream(side):
+                    for e, sl in self.slot_of[l].items():
+                        for dst, h in zip(self.hbm[l], self.host[l]):
+                            dst[sl].copy_(h[e], non_blocking=True)
+                    ev = torch.cuda.Event()
+                    ev.record(side)
+                self._pending[l] = ev
+            return
+        n = min(chunk, E)
+        stage = [[torch.empty(n, *sh, dtype=dt, pin_memory=True) for sh, dt in self.specs] for _ in range(2)]
+        done = [None, None]
+        k = 0
+        for l, jl in enumerate(src):
+            for e0 in range(0, E, n):
+                m = min(n, E - e0)
+                b = k % 2
+                if done[b] is not None:
+                    done[b].synchronize()            # the copy that last read this buffer has finished
+                jnf.read_experts(jl, range(e0, e0 + m), stage[b][0], stage[b][1], verify=verify)
+                with torch.cuda.stream(side):
+                    for dst, st in zip(self.hbm[l], stage[b]):
+                        dst[e0:e0 + m].copy_(st[:m], non_blocking=True)
+                    ev = torch.cuda.Event()
+                    ev.record(side)
+                done[b] = ev
+                k += 1
+        for ev in done:
+            if ev is not None:
+                ev.synchronize()
 
     def _store(self, l, e0, parts):
         n = parts[0].shape[0]

@@ -144,3 +144,32 @@ def test_tiered_ledger_matches_resident(gpu, int4):
     b.status()
     assert tier.stats["promotions"] > 0 and tier.stats["evictions"] > 0
     assert torch.equal(res.heat, tier.heat)
+
+
+def test_jnf_filled_ledgers_match_seeded(gpu, tmp_path):
+    """A JNF v1 tree written from a seeded ledger fills a resident and a tiered ledger
+    (verified reads, double-buffered staging / the pinned host tier) whose decodes give the
+    seeded ledger's bits, before and after promotions from the file-filled host tier."""
+    from tarfa_amd.jnf import JnfModel, write_jnf
+    L, T = 2, 4
+    res = ResidencyLedger(SHAPE, L, gpu)
+    res.fill_seeded(8)
+    write_jnf(tmp_path, {l: (res.hbm[l][0], res.hbm[l][1]) for l in range(L)}, top_k=SHAPE.top_k,
+              model_id="seeded-8", revision="0", tokenizer_revision="0")
+    jnf = JnfModel(tmp_path, SHAPE)
+    full = ResidencyLedger(SHAPE, L, gpu)
+    full.load_jnf(jnf, chunk=6)                      # 32 experts in chunks of 6: a ragged last chunk
+    tier = ResidencyLedger(SHAPE, L, gpu, hbm_slots=4)
+    tier.load_jnf(jnf)
+    torch.cuda.synchronize(gpu)
+    for l in range(L):
+        assert torch.equal(full.hbm[l][0], res.hbm[l][0]) and torch.equal(full.hbm[l][1], res.hbm[l][1])
+    layers = _layers(SHAPE, L, 8, gpu)
+    stacks = [MoEStack(g, layers) for g in (res, full, tier)]
+    logits, _ = zipf_logits(SHAPE, L, T, seed=6, device=gpu)
+    x0 = seeded.make_tokens(SHAPE, 8, T, device=gpu)
+    for t in range(T):
+        ys = [s.decode(x0[t:t + 1], logits[t]).clone() for s in stacks]
+        assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2]), f"token {t}"
+        if t == 1:
+            assert tier.promote(1, stacks[2].ids[1].tolist())
