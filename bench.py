@@ -15,7 +15,8 @@ T=4096 exact-BF16 prefill chunk through the same layer shape (router logits
 supplied ~N(0,1)), and the reference's op sequence run on the host CPU (torch
 bf16) on a bounded sample as ``cpu_baseline``.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-int4] [--no-stack]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-int4]
+                    [--no-small] [--no-stack]
 """
 import argparse
 import ctypes
@@ -135,6 +136,10 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-int4", action="store_true")
+    ap.add_argument("--no-small", action="store_true")
+    ap.add_argument("--small-steps", type=int, default=200,
+                    help="timed steps per token count of the small-batch leg")
+    ap.add_argument("--small-tokens", default="2,4,8,16", help="token counts of the small-batch leg (2..16)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain device copies of known size (scale for HBM byte counters)")
     return ap.parse_args(argv)
@@ -356,6 +361,12 @@ def run(args, log):
         log(f"prefill: {pus:.1f} us/layer, {tflops:.1f} TFLOP/s, weights {wgbs:.0f} GB/s")
         del pws, px, plg
 
+    # ---------------- small batches: T = 2..16 tokens through the full-size layer (router from
+    # weights, shared expert), layers rotated as in the headline; each expert the batch hits is
+    # read once, so the floor is (distinct experts + shared expert) x 3 H I bf16 + the router
+    if not args.no_small:
+        result["small_batch"] = small_batch(args, torch, seeded, shape, ledger, layers, tables, L, dev, lib, log)
+
     # ---------------- the whole stack: 48 resident layers, batch-1 decode of consecutive tokens,
     # per-layer router logits with Zipf(1.1) expert popularity (heat ledger + route telemetry on)
     if not args.no_stack:
@@ -389,6 +400,62 @@ def run(args, log):
 
     torch.cuda.synchronize()
     return result
+
+
+def small_batch(args, torch, seeded, shape, ledger, layers, tables, L, dev, lib, log):
+    """Small-batch decode (T = 2, 4, 8, 16 tokens per call) through the full-size layer:
+    router + routed experts + shared expert + combine, µs per layer and against the weight
+    read of the experts actually hit."""
+    from tarfa_amd.moe import Workspace
+    H, E, I, k, Is = shape.hidden, shape.num_experts, shape.intermediate, shape.top_k, shape.shared_intermediate
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = lib().tmoe_moe_block_bf16
+    expert_b = 2 * 3 * H * I
+    out = {"workload": "T tokens per call through the full-size exact-BF16 layer (router from weights, shared "
+                       "expert, combine in ascending expert id), layers rotated; floor = (distinct experts hit "
+                       "+ shared expert) x 3 H I bf16 + router weights at 8 TB/s", "by_tokens": {}}
+    K, W = args.small_steps, 16
+    for T in [int(v) for v in args.small_tokens.split(",")]:
+        ws = Workspace(shape, dev, tokens=T)
+        xs = [seeded.make_tokens(shape, 4, T, layer=l, device=dev) for l in range(L)]
+        o = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        ids = torch.empty(T, k, dtype=torch.int64, device=dev)
+        wts = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+        argv = [(xs[l].data_ptr(), T, layers[l].router_w.data_ptr(), None, tables[l].data_ptr(),
+                 *[t.data_ptr() for t in layers[l].shared], H, E, I, k, Is, o.data_ptr(), ids.data_ptr(),
+                 wts.data_ptr(), None, ws.buf.data_ptr(), ws.buf.numel(), stream) for l in range(L)]
+        hits = []
+        for l in range(min(L, 16)):
+            if fn(*argv[l]):
+                raise RuntimeError("tmoe_moe_block_bf16 failed")
+            hits.append(len(set(ids.view(-1).tolist())))
+        nh = sum(hits) / len(hits)
+
+        def go(i):
+            if fn(*argv[i % L]):
+                raise RuntimeError("tmoe_moe_block_bf16 failed")
+
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for i in range(W):
+            go(i)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(W, W + K):
+            go(i)
+        e1.record()
+        torch.cuda.synchronize()
+        ws.status()
+        us = e0.elapsed_time(e1) * 1e3 / K
+        floor_b = (nh + (1 if Is else 0)) * expert_b + 2 * E * H
+        floor_us = floor_b / (HBM_PEAK_GBS * 1e3)
+        out["by_tokens"][str(T)] = {"us_per_layer": round(us, 2), "us_per_token": round(us / T, 2),
+                                    "experts_hit": round(nh, 2), "weight_bytes": int(floor_b),
+                                    "floor_us": round(floor_us, 2), "frac_of_floor": round(floor_us / us, 4),
+                                    "steps": K}
+        log(f"small batch T={T}: {us:.1f} us/layer ({us / T:.1f} us/token), {nh:.1f} experts, "
+            f"{floor_us / us:.3f} of the weight-read floor")
+        del ws, xs
+    return out
 
 
 def cpu_baseline(args, torch, seeded, shape, ledger, layers, nbytes, dev, log):

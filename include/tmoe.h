@@ -105,8 +105,9 @@ int tmoe_dispatch(const int64_t* ids, int T, int k, int E, int32_t* offsets, int
  * x [T,H] bf16, ids [T,k] int64 (sentinel E skipped), weights [T,k] bf16, out [T,H] bf16.
  *   T == 1: per routed expert in router order, bf16(F.linear(bf16(silu(g))*u, Wd)),
  *           acc = bf16(acc + bf16(w_j * d_j))                (fused_int4.py:192-194)
- *   T  > 1: dispatch, grouped GEMM, and per token bf16 adds in ascending expert id
- *           (index_add_, fused_int4.py:239-244)
+ *   T  > 1: per token bf16 adds in ascending expert id (index_add_, fused_int4.py:239-244);
+ *           2 <= T <= 16 with H, I multiples of 128 (bf16) streams each expert hit once
+ *           (small-batch kernels), larger T runs dispatch and the grouped GEMM
  */
 int tmoe_experts_forward_bf16(const void* x, int T, const int64_t* ids, const void* weights,
                               const uint64_t* expert_table, int H, int E, int I, int k, void* out,
@@ -226,7 +227,7 @@ int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float eps, const
  * device array inside the library, TMOE_STATIC_SCRATCH_BYTES per GPU, held by each GPU
  * the library runs on until the process ends.  Nothing is allocated by the call.
  *   - Calls needing a larger workspace than the static one (tmoe_workspace_bytes(T, ...)
- *     > TMOE_STATIC_SCRATCH_BYTES; at H=2560, E=256, I=Is=1024, k=8 that is T > 221)
+ *     > TMOE_STATIC_SCRATCH_BYTES; at H=2560, E=256, I=Is=1024, k=8 that is T > 220)
  *     return TMOE_ERR_SCRATCH before any launch.
  *   - `status`: a caller-owned device uint32 (4-byte aligned, required) into which the
  *     kernels OR device-detected conditions: 1 = an expert id outside [0, E] (cannot come

@@ -20,6 +20,13 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
 int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
 int rmsnorm_launch(const uint16_t* h, const uint16_t* w, float eps, int T, int H, uint16_t* x, hipStream_t s);
 int residual_add_launch(const uint16_t* h, uint16_t* y, size_t n, hipStream_t s);
+bool sb_supported(int T, int H, int I, int Is, int k, int q4);
+int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
+              const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
+              const uint16_t* sh_down, const uint16_t* sh_gate_w, int H, int E, int I, int k, int Is,
+              uint16_t* out, void* ws, hipStream_t s, const uint16_t* resid, uint32_t* err);
+int sb_router_launch(const uint16_t* x, const uint16_t* wg, int T, int H, int E, int I, int k, int Is,
+                     int64_t* ids64, uint16_t* wb, uint32_t* heat, void* ws, hipStream_t s);
 }  // namespace tmoe
 
 
@@ -37,6 +44,16 @@ static int decode(DecodeParams& p, bool run_router, hipStream_t s) {
     if (st != TMOE_ERR_SHAPE) return st;
   }
   return decode_launch(p, run_router, s);
+}
+
+// 2 <= T <= 16 (bf16 experts): the two-launch small-batch path unless TMOE_SMALLBATCH=0
+// (the grouped-GEMM path, kept for comparison) or the shape has no small-batch variant.
+static bool small_batch(int T, int H, int I, int Is, int k, int q4) {
+  static const bool off = [] {
+    const char* v = getenv("TMOE_SMALLBATCH");
+    return v && v[0] == '0';
+  }();
+  return !off && sb_supported(T, H, I, Is, k, q4);
 }
 
 static bool misaligned(const void* p) { return ((uintptr_t)p & 15u) != 0; }
@@ -127,6 +144,9 @@ static int experts_forward(const void* x, int T, const int64_t* ids, const void*
     bind_ws(p, workspace, L);
     return q4 ? decode_fused_launch(p, false, s) : decode(p, false, s);
   }
+  if (small_batch(T, H, I, 0, k, q4))
+    return sb_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table, nullptr,
+                     nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, nullptr, nullptr);
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
                         nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4, nullptr,
                         nullptr);
@@ -218,6 +238,20 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
   int32_t* ids32 = ws_ptr<int32_t>(workspace, L.ids);
   float* wf = ws_ptr<float>(workspace, L.wts);
   float* gs = ws_ptr<float>(workspace, L.gs);
+  if (small_batch(T, H, I, Is, k, q4)) {
+    // Router (logits and top-k in one launch), then the small-batch experts; the shared gate
+    // is computed inside.
+    if (logits_in) {
+      if (int st = launch_router_topk(logits_in, T, E, k, ids_out, (uint16_t*)weights_out, ids32, wf, heat, s))
+        return st;
+    } else if (int st = sb_router_launch((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, I, k, Is, ids_out,
+                                         (uint16_t*)weights_out, heat, workspace, s)) {
+      return st;
+    }
+    return sb_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
+                     (const uint16_t*)sh_up, (const uint16_t*)sh_down, (const uint16_t*)sh_gate_w, H, E, I, k, Is,
+                     (uint16_t*)out, workspace, s, ln_w ? (const uint16_t*)h : nullptr, err);
+  }
   const float* lg = logits_in;
   if (!lg) {
     if (int st = launch_router_logits((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, logits, s)) return st;

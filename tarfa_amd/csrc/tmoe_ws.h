@@ -14,14 +14,19 @@ enum StatusSlot {
 };
 enum ErrorBit { kErrExpertId = 1u, kErrTimeout = 2u };
 
-// Synchronisation lines of the fused decode task graph.  Every counter owns a
-// 256-byte line (64 uint32): atomics on one hot line serialise at ~11 ns each.
-// Counters are zero between calls (the last wave to leave a queue re-zeroes its
-// exit count).  Hand-off words
+// Synchronisation lines (the fused decode's task graph, the small-batch arrivals), at a
+// fixed offset for every T so that calls of different sizes on one workspace never see
+// another call's data in them.  Every counter owns a 256-byte line (64 uint32): atomics on
+// one hot line serialise at ~11 ns each.  Counters are zero between calls (the last wave to
+// leave a queue re-zeroes its exit count; the last small-batch block of a token or column
+// tile re-zeroes its arrival count).  Hand-off words
 // (logits, activations, per-slot down results) are 64-bit {payload,
 // tag}: the tag is the call's epoch, so words left by earlier calls never match
 // and nothing is cleared between calls.
 constexpr int kLine = 64;                 // uint32 per line
+// Small-batch path: 2 <= T <= kSbMaxTokens tokens, T * k <= kSbMaxEntries, at most kSbTiles
+// combine tiles of 64 output columns.
+constexpr int kSbMaxTokens = 16, kSbMaxEntries = 256, kSbTiles = 4096 / 64;
 constexpr int kLogitReplicas = 32;        // router logits published to this many copies (blocks poll one each)
 constexpr int kQueues = 32;               // task queues: 4 waves x 8 XCD-sized groups of blocks
 enum SyncLine {
@@ -29,7 +34,9 @@ enum SyncLine {
   kLnQueuesDone = 1,                      // queues fully drained this call
   kLnQueue = 2,                           // [kQueues] word kQueueEpochWord: epoch copy for the queue's waves
   kLnQueueExit = kLnQueue + kQueues,      // [kQueues] waves that left each queue
-  kSyncLines = kLnQueueExit + kQueues,
+  kLnSbRouter = kLnQueueExit + kQueues,   // [kSbMaxTokens] small-batch router blocks arrived, per token
+  kLnSbTile = kLnSbRouter + kSbMaxTokens, // [kSbTiles] small-batch down blocks arrived, per column tile
+  kSyncLines = kLnSbTile + kSbTiles,
 };
 // Each queue line also carries a copy of the epoch, read by that queue's waves
 // (coherent loads of one line serialise, so 2048 waves must not share one word).
@@ -70,6 +77,9 @@ struct Ws {
   size_t ch;       // bf16[T * k * H]    per-assignment expert outputs, unscaled (T > 1)
   size_t desc;     // int32x4[T * k / 64 + E + T / 64 + 2]   prefill M-chunk descriptors (T > 1)
   size_t xn;       // bf16[T * H]        RMSNorm of the hidden state (the layer entry points)
+  size_t sbord;    // small-batch combine order: int32 rows[kSbMaxEntries], f32 weights[kSbMaxEntries],
+                   // int32 counts[kSbMaxTokens]; then the down kernel's slice descriptors
+                   // (16 bytes each: a header and up to kSbMaxEntries + 2 slices)
   size_t total;
 };
 
@@ -97,6 +107,7 @@ inline Ws ws_layout(int T, int H, int E, int I, int k, int Is) {
   w.ch = take(t > 1 ? 2 * t * (size_t)k * (size_t)H : 0);
   w.desc = take(t > 1 ? 16 * (t * (size_t)k / 64 + (size_t)E + t / 64 + 2) : 0);
   w.xn = take(2 * t * (size_t)H);
+  w.sbord = take(4 * (2 * (size_t)kSbMaxEntries + kSbMaxTokens) + 16 * ((size_t)kSbMaxEntries + 3));
   w.total = o;
   return w;
 }

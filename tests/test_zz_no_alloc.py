@@ -53,7 +53,7 @@ def test_noalloc_block_rejects_what_it_cannot_hold(gpu):
     layer = seeded.make_layer(MoEShape(2560, 256, 1024, 8, 1024), 91, device=gpu)
     layer.table = tm.expert_table(layer.gate_up, layer.down)
     status = torch.zeros(1, dtype=torch.int32, device=gpu)
-    x = seeded.make_tokens(FULL, 91, 222, device=gpu)          # one token past the static scratch
+    x = seeded.make_tokens(FULL, 91, 221, device=gpu)          # one token past the static scratch
     assert _noalloc(FULL, x, layer, status)[0] == TMOE_ERR_SCRATCH
     assert "static scratch" in lib().tmoe_strerror(TMOE_ERR_SCRATCH).decode()
     st = lib().tmoe_moe_block_bf16_noalloc(x.data_ptr(), 1, layer.router_w.data_ptr(), None,
