@@ -42,16 +42,20 @@
 //     are normally complete); stale words are re-polled with coherent loads.
 //   - Each wave caches the routing; the block's copy in LDS is resolved once.
 //   - Queue q (of 32) is served by wave q % 4 of the blocks b with b % 8 == q / 4
-//     (one XCD) and holds tasks q, q + 32, ...; the wave of rank r = b / 8 among
-//     its queue's `users` takes ticket r first.  In exact-bf16 mode every later
-//     ticket is drawn from the queue's counter (users + draw), so tasks start in
-//     list order; the draw for the next task is issued when a task starts and read
-//     after the task's loads, before its stores (gfx9 counts stores in vmcnt, and
-//     vector memory returns in issue order).  In int4 mode the tickets are static:
-//     r + users, r + 2 users, ...  Either way tickets of a queue are taken in
-//     increasing order, a task only waits on tasks with smaller indices, and the
-//     grid fits on the GPU at once, so the smallest unfinished task is always some
-//     running wave's current or next task and can finish.
+//     (one XCD) and holds tasks q, q + 32, ...  In exact-bf16 mode every ticket, a
+//     wave's first included, is drawn from the queue's counter: the first at entry
+//     (its round trip overlaps the epoch load), every later one when a task starts,
+//     read after the task's loads and before its stores (gfx9 counts stores in
+//     vmcnt, and vector memory returns in issue order).  A queue's tasks are so
+//     claimed in list order and only by running waves, and a task waits only on
+//     tasks with smaller indices: the smallest unfinished task is always some running
+//     wave's current task and can finish, whatever subset of the grid is resident,
+//     as long as every queue has one running wave (one block of the grid on each XCD;
+//     tests/test_ticket_progress.py simulates the task graph).  In int4 mode the
+//     tickets are static, r + users i for the wave of rank r = b / 8 (a dynamic draw
+//     per task costs the short int4 tasks 26.7 -> 31.3 us), which relies on the whole
+//     grid being resident: the launch sizes it from the occupancy (kBlocksPerCU), and
+//     a wait that still starves (another kernel holding CUs) ends in kErrTimeout.
 //   - Every poll backs off and is bounded (kErrTimeout on expiry).
 //   - The last wave to leave a queue re-zeroes its exit count; the last queue to
 //     drain advances the epoch.
@@ -80,10 +84,9 @@ constexpr int q4_down_rows(int MI) { return MI <= 2 ? 16 : 8; }
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
-// Tickets after a wave's first: drawn from a per-queue counter (tasks then start
-// in list order; exact-bf16 mode) or static (rank + users * i; int4 mode, where
-// waves that reach down tasks early keep their weight loads in flight while the
-// gate/up tasks finish).
+// Tickets: every one drawn from a per-queue counter (exact-bf16 mode) or static
+// (rank + users * i; int4 mode, where the draw's round trip is not hidden by the short
+// tasks' loads).
 template <bool Q4>
 constexpr bool dynamic_tickets() { return !Q4; }
 constexpr int kBlocksPerCU = 2;        // resident blocks per CU (bounds the bytes in flight per XCD)
@@ -853,6 +856,16 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   uint32_t* queue = line(p, kLnQueue + q);
   const uint32_t users = (gridDim.x - (uint32_t)(q / kWaves) + 7u) / 8u;
   const uint32_t rank = blockIdx.x / 8u;
+  constexpr bool DYN = dynamic_tickets<Q4>();
+  uint32_t* draw = line(p, kLnQueueExit + q) + kQueueDrawWord;
+  // Exact-bf16 mode: the first ticket, drawn at once; read where the first task starts.
+  uint32_t first = 0;
+  if (DYN && lane0 == 0) {
+    uintptr_t a = reinterpret_cast<uintptr_t>(draw);
+    asm volatile("" : "+v"(a));
+    first = __hip_atomic_fetch_add(reinterpret_cast<__attribute__((address_space(1))) uint32_t*>(a), 1u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   // Every lane loads the epoch (one transaction); kept per lane, the value is
   // first waited for where a task stores or polls.
   const uint32_t tag = ld32c(queue + kQueueEpochWord) + 1u;
@@ -875,8 +888,6 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       rwc = p.w_in[lane0 - kRwW];
     }
   }
-  constexpr bool DYN = dynamic_tickets<Q4>();
-  uint32_t* draw = line(p, kLnQueueExit + q) + kQueueDrawWord;
   // The input fragment: loaded per task; with LN formed once per wave (the norm needs a
   // wave reduction over h) and kept in registers for the wave's later tasks.
   XPack<MH> xcache;
@@ -901,7 +912,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       have_x = true;
     }
   }
-  uint32_t ticket = rank;
+  uint32_t ticket = DYN ? (uint32_t)__builtin_amdgcn_readlane((int)first, 0) : rank;
   const uint64_t t_entry = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
   if (p.trace && blockIdx.x == 0 && wid == 0 && lane0 == 0) {
     const uint64_t hdr[kTraceHeader] = {(uint64_t)p.n_tasks, gridDim.x, (uint64_t)p.n_r, (uint64_t)p.n_s,
@@ -915,8 +926,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     if (t >= p.n_tasks) break;
     uint64_t ts_start = 0, ts_route = 0, ts_take = 0;
     if (p.trace) ts_start = __builtin_amdgcn_s_memrealtime();
-    // The next ticket: drawn now from the queue's counter (first tickets are the
-    // ranks), read after this task.  Vector memory returns in issue order, so the
+    // The next ticket: drawn now from the queue's counter, read after this task.  Vector memory returns in issue order, so the
     // task's own loads bring the draw back with them.
     uint32_t nxt = 0, nt = 0;
     bool got = !DYN;
@@ -1022,7 +1032,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       rec[6] = ticket;
       rec[7] = (uint64_t)tk.type | (uint64_t)(tk.slot + 1) << 8 | (uint64_t)tk.idx << 16;
     }
-    ticket = DYN ? users + nt : rank + users * (i + 1);
+    ticket = DYN ? nt : rank + users * (i + 1);
   }
   if (p.trace && lane0 == 0) {
     uint64_t* rec = p.trace + kTraceHeader + (size_t)p.n_tasks * kTraceTaskWords + 2 * ((size_t)blockIdx.x * kWaves + wid);
