@@ -102,6 +102,8 @@ struct SbGroups {
   int sgrp[256];         // slice s: its group
   int toks[16];          // this block's slice: token of row r
   int U, NS;             // groups, slices (routed)
+  int gent[256];         // group u: one of its entries
+  const uint16_t* ew[256];   // entry j: its expert's gate_up rows (loaded with the id)
 };
 
 __device__ __forceinline__ int sb_load_id(const SbParams& p, int j) {
@@ -124,6 +126,7 @@ __device__ void sb_groups(const SbParams& p, SbGroups& g) {
     ev[i] = j < n ? sb_load_id(p, j) : p.E;
   }
   bool bad = false;
+  const uint16_t* ew[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int j = tid + i * nthr;
@@ -133,6 +136,8 @@ __device__ void sb_groups(const SbParams& p, SbGroups& g) {
       e = -1;
     }
     if (j < 256) g.ids[j] = e;
+    // The expert's gate_up rows, requested now: the round trip overlaps the group work below.
+    ew[i] = e >= 0 ? reinterpret_cast<const uint16_t*>(p.table[2 * e]) : nullptr;
   }
   if (bad && blockIdx.x == 0) atomicOr(p.err, (uint32_t)kErrExpertId);
   __syncthreads();
@@ -157,7 +162,13 @@ __device__ void sb_groups(const SbParams& p, SbGroups& g) {
       const int u = sb_group_of(g, e);
       atomicOr(&g.gmask[u], 1u << (j / p.k));
       g.gexp[u] = e;
+      g.gent[u] = j;
     }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = tid + i * nthr;
+    if (j < 256) g.ew[j] = ew[i];
   }
   __syncthreads();
   if (tid < 64) {
@@ -267,14 +278,55 @@ __device__ __forceinline__ u32x4 sb_ld_coherent(const uint16_t* p) {
   return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
 }
 
-// Combine of output columns [c0, c0 + ncols) for every token, one thread per (token, 8
-// columns); the expert outputs are read with agent-scope loads.
-__device__ void sb_combine(const SbParams& p, int c0, int ncols) {
+// The combine order and the shared gate as the down kernel keeps them in LDS (loaded when a
+// wave starts, so the last wave of a tile combines with one round trip: its expert outputs).
+struct SbOrder {
+  int row[kSbMaxEntries];
+  float w[kSbMaxEntries];
+  int n[kSbMaxTokens];
+  float gs[kSbMaxTokens];
+};
+
+// The order held in registers from the wave's start: lane l keeps entries l + 64 i.
+struct SbOrderRegs {
+  int row[kSbMaxEntries / 64];
+  float w[kSbMaxEntries / 64];
+  int n;
+  float gs;
+  __device__ __forceinline__ void load(const SbParams& p, int lane) {
+    const int ne = p.T * p.k;
+#pragma unroll
+    for (int i = 0; i < kSbMaxEntries / 64; ++i) {
+      const int j = lane + 64 * i;
+      row[i] = j < ne ? p.ord_row[j] : 0;
+      w[i] = j < ne ? p.ord_w[j] : 0.f;
+    }
+    n = lane < p.T ? p.ord_n[lane] : 0;
+    gs = lane < p.T && p.sh_gate ? p.gs[lane] : 0.f;
+  }
+  __device__ __forceinline__ void store(SbOrder& o, int lane) const {
+#pragma unroll
+    for (int i = 0; i < kSbMaxEntries / 64; ++i) {
+      o.row[lane + 64 * i] = row[i];
+      o.w[lane + 64 * i] = w[i];
+    }
+    if (lane < kSbMaxTokens) {
+      o.n[lane] = n;
+      o.gs[lane] = gs;
+    }
+  }
+};
+
+// Combine of output columns [c0, c0 + ncols) for every token, one lane per (token, 8
+// columns): the shared expert's output, the residual and up to 8 expert outputs (agent-scope
+// loads) requested together, then added in rank order.
+__device__ void sb_combine(const SbParams& p, const SbOrder& o, int c0, int ncols) {
   const int H = p.H, k = p.k, chunks = ncols / 8;
   for (int job = threadIdx.x; job < p.T * chunks; job += blockDim.x) {
     const int t = job / chunks, col = c0 + (job - t * chunks) * 8;
-    const int nv = p.ord_n[t];
+    const int nv = o.n[t];
     const u32x4 vs = p.sh_gate ? sb_ld_coherent(p.sh + (size_t)t * H + col) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 hv = p.resid ? ld16(p.resid + (size_t)t * H + col) : u32x4{0u, 0u, 0u, 0u};
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -287,35 +339,28 @@ __device__ void sb_combine(const SbParams& p, int c0, int ncols) {
     // Eight entries' loads in flight at a time, added in rank order.
     for (int j0 = 0; j0 < nv; j0 += 8) {
       u32x4 v[8];
-      float wt[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j0 + j < nv) {
-          v[j] = sb_ld_coherent(p.ch + (size_t)p.ord_row[t * k + j0 + j] * H + col);
-          wt[j] = p.ord_w[t * k + j0 + j];
-        }
-      }
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (j0 + j < nv) add(v[j], wt[j]);
+        if (j0 + j < nv) v[j] = sb_ld_coherent(p.ch + (size_t)o.row[t * k + j0 + j] * H + col);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j0 + j < nv) add(v[j], o.w[t * k + j0 + j]);
     }
-    if (p.sh_gate) add(vs, p.gs[t]);
+    if (p.sh_gate) add(vs, o.gs[t]);
     if (p.resid) {   // the layer's residual add: bf16(h + y)
-      const u32x4 hv = ld16(p.resid + (size_t)t * H + col);
       const float hx[8] = {bf16_lo(hv.x), bf16_hi(hv.x), bf16_lo(hv.y), bf16_hi(hv.y),
                            bf16_lo(hv.z), bf16_hi(hv.z), bf16_lo(hv.w), bf16_hi(hv.w)};
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = hx[i] + acc[i];
     }
-    u32x4 o;
-    o.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
-    o.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
-    o.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
-    o.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
-    *reinterpret_cast<u32x4*>(p.out + (size_t)t * H + col) = o;
+    u32x4 out;
+    out.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+    out.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+    out.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+    out.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+    *reinterpret_cast<u32x4*>(p.out + (size_t)t * H + col) = out;
   }
 }
-
 
 // Up: one wave per (slice, 8 activation columns) = 8 gate and 8 up weight rows over K = H
 // (128 nkb columns, R stages in flight); block 0 also writes the combine order and the down
@@ -358,7 +403,7 @@ __global__ __launch_bounds__(64) void k_sb_up(SbParams p) {
     mask = g.gmask[u];
     ms = min(kSbSlice, __popc(mask) - kSbSlice * sj);
     arow0 = (size_t)(g.gpre[u] + kSbSlice * sj) * I;
-    gate = reinterpret_cast<const uint16_t*>(p.table[2 * g.gexp[u]]);
+    gate = g.ew[g.gent[u]];
     up = gate + (size_t)I * H;
   }
   sb_tokens(g, mask, kSbSlice * sj, ms);
@@ -441,17 +486,24 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
   __shared__ u32x4 bt[32 * 17];                       // a stage's 32 weight rows x 16 chunks, rows padded
   __shared__ u32x4 at[8 * 17];                        // a stage's activations, chunks x rows
   __shared__ __align__(16) uint16_t dt[16][32];      // the outputs, rows x columns
+  __shared__ SbOrder so;                              // the combine order (for the tile's last wave)
   const int lane = threadIdx.x;
   const int H = p.H, I = p.I, nkb = I / 128;
   const int tiles = H / 32;
   const int si = blockIdx.x / tiles, tile = blockIdx.x - si * tiles;
   const int total = (int)p.slices[0].arow;
+  SbOrderRegs ordr;
   if (si >= total) {
     // No slice at all: the output is zero (plus the residual).
-    if (total == 0 && si == 0 && (tile & 1) == 0) sb_combine(p, tile * 32, 64);
+    if (total == 0 && si == 0 && (tile & 1) == 0) {
+      ordr.load(p, lane);
+      ordr.store(so, lane);
+      sb_combine(p, so, tile * 32, 64);
+    }
     return;
   }
   const SbSlice d = p.slices[1 + si];
+  ordr.load(p, lane);
   const int ms = d.ms;
   const int n = lane & 15, q = lane >> 4;
   const int rr = min(n, ms - 1);
@@ -519,7 +571,8 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
   if (lane == 0) prev = __hip_atomic_fetch_add(p.cnt + ct * kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   prev = __shfl(prev, 0);
   if (prev != arrivals - 1u) return;
-  sb_combine(p, ct * 64, 64);
+  ordr.store(so, lane);
+  sb_combine(p, so, ct * 64, 64);
   if (lane == 0) __hip_atomic_store(p.cnt + ct * kLine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -619,12 +672,9 @@ int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids
   sb_launch_up(p, sb_ring(H / 128, 5), dim3((unsigned)((nshs + slices) * (I / 8))), s);
   {
     const dim3 grid((unsigned)((nshs + slices) * (H / 32)));
-    switch (sb_ring(I / 128, 4)) {
-      case 4: hipLaunchKernelGGL((k_sb_down<4>), grid, dim3(64), 0, s, p); break;
-      case 3: hipLaunchKernelGGL((k_sb_down<3>), grid, dim3(64), 0, s, p); break;
-      case 2: hipLaunchKernelGGL((k_sb_down<2>), grid, dim3(64), 0, s, p); break;
-      default: hipLaunchKernelGGL((k_sb_down<1>), grid, dim3(64), 0, s, p); break;
-    }
+    // Two stages of 32 rows in flight (deeper rings measured no faster and cost a wave slot).
+    if (sb_ring(I / 128, 2) == 2) hipLaunchKernelGGL((k_sb_down<2>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((k_sb_down<1>), grid, dim3(64), 0, s, p);
   }
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
