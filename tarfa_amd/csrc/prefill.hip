@@ -11,6 +11,8 @@
 //             rounding after each add, then + sh          fused_int4.py:244 (index_add_),
 //                                                          transformers/.../modeling_qwen3_5_moe.py:796
 // The shared expert is one more group (id E) whose rows are all T tokens in order.
+#include <stdlib.h>
+#include <string.h>
 #include <type_traits>
 #include "tmoe_gemv.h"
 #include "tmoe_ws.h"
@@ -195,6 +197,7 @@ struct GemmParams {
   uint16_t* out;             // up: act; down: ch [T*k, H], each expert output unscaled
   uint16_t* out_sh;          // down: sh [T, H], the shared expert's output before its gate
   const int4* desc;          // persistent kernel: M-chunk descriptors {group, rows, first row, 0}
+  uint16_t* sink;            // 16 bytes nobody reads: whole-line kernel stores of rows past a tile
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -545,6 +548,13 @@ __device__ __forceinline__ void gdma16(const void* sbase, uint32_t voff, const v
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(l) : "memory");
 }
 
+// 16 bytes per lane into LDS at lds + OFS (an LDS write the compiler does not reorder with
+// the pipeline's asm loads and waits).
+template <int OFS>
+__device__ __forceinline__ void dsw16(uint32_t lds, const u32x4& v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(lds), "v"(v), "n"(OFS) : "memory");
+}
+
 // One wave's view of one tile (all wave-uniform).
 struct PTile {
   int arow0;                // A row of the tile's first row (gather: its position in perm)
@@ -877,6 +887,323 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   wait_vmcnt<0>();   // the last, unused stages landed before the block's LDS is released
 }
 
+// ---------------------------------------------------------------- grouped GEMM, whole-line weights
+// Exact-bf16 twin of k_grouped_gemm_p (same tiles, descriptors, tile order and outputs), built
+// around how HBM serves the weights: a load instruction reading 16 rows x 64 bytes (an MFMA
+// fragment) streams at ~5-6 TB/s, one reading whole 128-byte lines of 8 rows at ~7 TB/s.
+//   Weights: per 64-wide K stage a wave reads its 32 rows x 128 bytes with 4 whole-line loads
+//   (load i, lane l: row 8 i + l / 8, bytes 16 (l % 8)), kWB stages ahead in registers.  At
+//   its stage the wave writes them to its own 4 KB LDS region, row r's 16-byte chunk c at
+//   chunk c ^ (r % 8), and reads them back as MFMA fragments (16 rows, one chunk): the
+//   swizzle of the A slots, conflict-free both ways.  Only the wave itself touches its
+//   region, and one wave's LDS operations complete in order.
+//   A: as in k_grouped_gemm_p (direct global -> LDS loads of whole rows), in a ring of kWAS
+//   slots requested kWA stages ahead; the slot is a run-time index (stage % kWAS).
+// Iteration g: request A stage g + kWA; wait for weight stage g; its registers to the region;
+// request weight stage g + kWB into them; 40 MFMAs; wait for A stage g + 1; barrier.
+// K: a multiple of 4 stages (256) and at least 8 stages (the next tile's perm words, requested
+// after a tile's epilogue, are used before its last cycle, 4 stage waits later).
+constexpr int kWB = 4;                        // weight stages in registers (the unrolled cycle)
+constexpr int kWAS = 5;                       // A ring slots
+constexpr int kWA = kWAS - 1;                 // A stages requested ahead (= kWB: every request
+                                              // past a tile's end falls in its last cycle)
+constexpr int kWBLoads = 2 * kPNB;            // weight loads per wave per stage (8 rows each)
+constexpr int kWReg = 16 * kPNB * 8;          // u32x4 per wave region (32 rows x 128 B)
+constexpr int kWOps = kPLoads + kWBLoads;     // vector memory operations per stage
+static_assert(kWA == kWB, "A and weight stages requested equally far ahead");
+static_assert(kWBLoads + (kWA - 1) * kWOps < 64 && (kWB - 1) * kWOps + kPLoads < 64, "vmcnt range");
+static_assert((kWAS * kPSlot + kPW * kWReg) * 16 <= 160 * 1024, "LDS");
+
+template <bool UP>
+__global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
+  __shared__ u32x4 lA[kWAS * kPSlot];
+  __shared__ u32x4 lB[kPW * kWReg];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = p.K;
+  u32x4* const reg = lB + wid * kWReg;
+
+  const int c_lo = sload1(p.tile_start + p.group_lo);
+  const int c_hi = sload1(p.tile_start + p.group_hi);
+  const int total = (c_hi - c_lo) * p.n_ntiles;
+  const int nbx = (int)gridDim.x >> 3;
+  const int xcd = (int)blockIdx.x & 7, qb = (int)blockIdx.x >> 3;
+  const int per_xcd = (total + 7) / 8;
+  const int f0 = xcd * per_xcd + qb;
+  const int f_end = min(total, (xcd + 1) * per_xcd);
+  if (f0 >= f_end) return;
+  const int ntile = (f_end - f0 + nbx - 1) / nbx;
+
+  auto tile = [&](int j) {
+    const int f = f0 + j * nbx;
+    const int mt = c_lo + f / p.n_ntiles, nt = f % p.n_ntiles;
+    const i32x4 d = sload4(p.desc + mt);
+    const int g = d.x, row0 = d.z;
+    const bool shared = g == p.E;
+    PTile t;
+    t.m = d.y;
+    t.gather = p.up && !shared;
+    t.arow0 = (!p.up && shared ? p.shared_row0 : 0) + row0;
+    const int c0 = p.up ? nt * kPUpCols + wid * 16 : nt * kPDnCols + wid * 32;
+    if (p.up) t.o = p.out + (size_t)(shared ? p.shared_row0 + row0 : row0) * p.N + nt * kPUpCols;
+    else t.o = (shared ? p.out_sh : p.out) + (size_t)row0 * p.N + nt * kPDnCols;
+    const uint16_t *w0, *w1;
+    if (shared) {
+      w0 = p.shw0;
+      w1 = p.up ? p.shw1 : p.shw0;
+    } else {
+      w0 = w1 = reinterpret_cast<const uint16_t*>(sload_ptr(p.table + 2 * g + (p.up ? 0 : 1)));
+    }
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) {
+      const int wr = p.up ? ((nb && !shared) ? p.I : 0) + c0 : c0 + 16 * nb;
+      t.b[nb] = (nb ? w1 : w0) + (size_t)wr * K;
+      t.q[nb] = nullptr;
+      t.sc[nb] = nullptr;
+    }
+    return t;
+  };
+
+  PTile cur, nxt;
+  // Lane constants.  A: load j covers rows 8 x .. 8 x + 7 (x = wid + 8 j, the last four
+  // repeating 16..19); weights: load 2 nb + h covers rows 16 nb + 8 h + lane / 8 of the
+  // wave's two blocks, bytes 16 (lane % 8).
+  const int lrow = lane & 15;
+  int a_row[kPLoads];
+#pragma unroll
+  for (int j = 0; j < kPLoads; ++j) {
+    const int x = wid + kPW * j;
+    a_row[j] = 8 * (x < kBM / 8 ? x : x - kPW / 2) + (lane >> 3);
+  }
+  const int a_col = 8 * ((lane & 7) ^ (lane >> 3));
+  const int rd0 = lrow * 8 + ((lane >> 4) ^ (lrow & 7));          // fragment chunk, k 0..31
+  const int rd1 = lrow * 8 + ((4 + (lane >> 4)) ^ (lrow & 7));    // k 32..63
+  const int wr_off = (lane >> 3) * 8 + ((lane & 7) ^ (lane >> 3)); // region chunk of load i: + 64 i
+  uint32_t b_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) b_off[h] = (uint32_t)(((8 * h + (lane >> 3)) * K + (lane & 7) * 8) * 2);
+
+  f32x4 acc[kPMB][kPNB];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < kPMB; ++i)
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb) acc[i][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  u32x4 breg[kWB][kWBLoads];
+  const int nk = K / kBK;   // a multiple of kWB, at least 2 kWB
+  uint32_t a_off_cur[kPLoads], a_off_nxt[kPLoads];
+  uint32_t pv_cur[kPLoads], pv_nxt[kPLoads];
+  // Always kPLoads loads (tiles without a gather read perm[0]): the waits count them.
+  auto fetch_perm = [&](uint32_t* pv, const PTile& t) {
+    const int32_t* pp = p.perm + (t.gather ? t.arow0 : 0);
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) pv[j] = gld4(pp, t.gather ? (uint32_t)(min(a_row[j], t.m - 1) * 4) : 0u);
+  };
+  auto a_offsets = [&](uint32_t* o, uint32_t* pv, const PTile& t) {
+    asm volatile("" : "+v"(pv[0]), "+v"(pv[1]), "+v"(pv[2]));
+    static_assert(kPLoads == 3, "three perm words per lane");
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) {
+      const int row = t.gather ? (int)pv[j] / p.k : t.arow0 + min(a_row[j], t.m - 1);
+      o[j] = (uint32_t)row * (uint32_t)(K * 2) + (uint32_t)(a_col * 2);
+    }
+  };
+  auto gaddr = [](const void* base, size_t ofs) { return reinterpret_cast<const char*>(base) + ofs; };
+  auto dma_a = [&](int slot, bool nx, int st) {
+    const char* ta = gaddr(p.a, (size_t)st * kBK * 2);
+    u32x4* const s = lA + slot * kPSlot;
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) {
+      const int x = wid + kPW * j;
+      gdma16(ta, nx ? a_off_nxt[j] : a_off_cur[j], s + (x < kBM / 8 ? x : x - kPW / 2) * 64);
+    }
+  };
+  auto load_b = [&](int bs, bool nx, int st) {
+    const size_t k0 = (size_t)st * kBK * 2;
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) {
+      const char* br = gaddr(nx ? nxt.b[nb] : cur.b[nb], k0);
+      breg[bs][2 * nb] = gld16(br, b_off[0]);
+      breg[bs][2 * nb + 1] = gld16(br, b_off[1]);
+    }
+  };
+  // Wait for weight stage bs (requested kWB - 1 iterations and one A group before, plus X
+  // operations of an epilogue in between).  The registers pass through the asm, so nothing
+  // reads them before the wait.
+  // Stores per thread in one epilogue (up: 2 passes x 3, down: 5 passes x 2); the first 4
+  // iterations of the next tile add them and the next tile's perm loads (kXH) to their waits.
+  constexpr int kEpiStores = UP ? 6 : 10;
+  constexpr int kXH = kEpiStores + kPLoads;
+  auto wait_b = [&](int bs, bool head) {
+    constexpr int n = (kWB - 1) * kWOps + kPLoads;
+    static_assert(kWBLoads == 4 && n + kXH < 64, "four weight registers per stage; vmcnt range");
+    if (head)
+      asm volatile("s_waitcnt vmcnt(%4)"
+                   : "+v"(breg[bs][0]), "+v"(breg[bs][1]), "+v"(breg[bs][2]), "+v"(breg[bs][3])
+                   : "n"(n + kXH));
+    else
+      asm volatile("s_waitcnt vmcnt(%4)"
+                   : "+v"(breg[bs][0]), "+v"(breg[bs][1]), "+v"(breg[bs][2]), "+v"(breg[bs][3])
+                   : "n"(n));
+  };
+  const uint32_t wr_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)(reg + wr_off);
+  auto to_region = [&](int bs) {
+    dsw16<0 * 1024>(wr_lds, breg[bs][0]);
+    dsw16<1 * 1024>(wr_lds, breg[bs][1]);
+    dsw16<2 * 1024>(wr_lds, breg[bs][2]);
+    dsw16<3 * 1024>(wr_lds, breg[bs][3]);
+  };
+  auto multiply = [&](int aslot) {
+    const u32x4* la = lA + aslot * kPSlot;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int rd = ks ? rd1 : rd0;
+      bf16x8_t b[kPNB];
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb) b[nb] = as_bf16x8(reg[nb * 128 + rd]);
+#pragma unroll
+      for (int i = 0; i < kPMB; ++i) {
+        const bf16x8_t a = as_bf16x8(la[i * 128 + rd]);
+#pragma unroll
+        for (int nb = 0; nb < kPNB; ++nb)
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[i][nb], 0, 0, 0);
+      }
+    }
+  };
+  auto barrier_raw = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // End of stage g: this wave's part of A stage g + 1 landed (requested kWA - 1 iterations
+  // before, followed by that iteration's weight loads and kWA - 1 whole iterations), then a
+  // raw barrier (every wave's part visible; every wave done reading the slot refilled next).
+  auto stage_end = [&](bool head) {
+    constexpr int n = kWBLoads + (kWA - 1) * kWOps;
+    static_assert(n + kXH < 64, "vmcnt range");
+    if (head) wait_vmcnt<n + kXH>();
+    else wait_vmcnt<n>();
+    barrier_raw();
+  };
+
+  // Epilogue through the wave regions (32 KB, free between a tile's last stage and the next
+  // tile's first), as in k_grouped_gemm_p: passes of BPP 16-row blocks, row r's 16-byte chunk
+  // q at chunk q ^ 2 ((r / 4) % 4); C fragment lane l holds rows 4 (l / 16) + e, column l % 16.
+  auto epilogue = [&](const PTile& t) {
+    constexpr int TCB = UP ? 2 * kPUpCols : 2 * kPDnCols;
+    constexpr int BPP = UP ? 5 : 2;
+    constexpr int RPP = 16 * BPP, CPR = TCB / 16;
+    constexpr int NST = (RPP * CPR + 64 * kPW - 1) / (64 * kPW);
+    static_assert(RPP * TCB <= kPW * kWReg * 16 && kPMB % BPP == 0, "a pass fits in the regions");
+    static_assert(NST * 64 * kPW / CPR * TCB <= kPW * kWReg * 16, "reads past the pass stay in the regions");
+    static_assert(NST * (kPMB / BPP) == kEpiStores, "stores per thread per epilogue");
+    char* stg = reinterpret_cast<char*>(lB);
+    const int sw = 2 * (lane >> 4), rl = 4 * (lane >> 4);
+    int cb[kPNB];
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) {
+      const int col = UP ? wid * 16 + lrow : wid * 32 + nb * 16 + lrow;
+      cb[nb] = rl * TCB + ((col >> 3) ^ sw) * 16 + (col & 7) * 2;
+    }
+#pragma unroll
+    for (int P = 0; P < kPMB / BPP; ++P) {
+#pragma unroll
+      for (int ii = 0; ii < BPP; ++ii) {
+        const int i = P * BPP + ii;
+        if (16 * i >= t.m) continue;   // padding rows only (their stores go to the sink)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          char* rowp = stg + (ii * 16 + e) * TCB;
+          if constexpr (UP) {
+            *reinterpret_cast<uint16_t*>(rowp + cb[0]) =
+                swiglu_bits_hw(acc[i][0][e], acc[i][1][e]);
+          } else {
+#pragma unroll
+            for (int nb = 0; nb < kPNB; ++nb)
+              *reinterpret_cast<uint16_t*>(rowp + cb[nb]) = f32_to_bf16(acc[i][nb][e]);
+          }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      barrier_raw();
+      // Exactly kEpiStores / passes stores per thread and pass, rows past the tile (and
+      // places past the pass) redirected to the sink: the next tile's first waits count them.
+#pragma unroll 1
+      for (int q = 0; q < NST; ++q) {
+        const int x = tid + q * 64 * kPW;
+        const int rr = x / CPR, qc = x - rr * CPR, row = P * RPP + rr;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * TCB + ((qc ^ (2 * ((rr >> 2) & 3))) * 16));
+        const bool ok = x < RPP * CPR && row < t.m;
+        *reinterpret_cast<u32x4*>(ok ? t.o + (size_t)row * p.N + qc * 8 : p.sink) = v;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      barrier_raw();
+    }
+  };
+
+  cur = tile(0);
+  nxt = tile(min(1, ntile - 1));
+  fetch_perm(pv_cur, cur);
+  wait_vmcnt<0>();
+  a_offsets(a_off_cur, pv_cur, cur);
+  // Prologue: iterations -kWA .. -1 in the loop's issue order (iteration v requests A stage
+  // v + kWA, then weight stage v + kWB), then what an epilogue leaves between a tile's last
+  // cycle and the next tile's first (kEpiStores stores, here to the sink, and the next
+  // tile's perm loads): every tile starts with the same operations in flight.
+#pragma unroll
+  for (int v = -kWA; v < 0; ++v) {
+    dma_a(v + kWA, false, v + kWA);
+    load_b(v + kWB, false, v + kWB);
+  }
+  {
+    const uint64_t sk = (uint64_t)(uintptr_t)p.sink;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < kEpiStores; ++q) asm volatile("global_store_dwordx4 %0, %1, off" : : "v"(sk), "v"(z) : "memory");
+  }
+  fetch_perm(pv_nxt, nxt);
+  stage_end(true);
+  // Stage counter continuous over tiles: A slot (stage % kWAS), weight slot (stage % kWB).
+  // Stages past a tile's end are the next tile's first ones (the last tile: its own first
+  // stages again, never multiplied); nk is a multiple of kWB, so tiles start on a cycle.
+  int aslot = 0;   // A slot of this iteration's stage; its A request goes to the slot before
+  // kHead: a tile's first cycle; its weight stages 0..3 and A stages 1..3 were requested
+  // before the previous epilogue's stores and this tile's successor's perm loads (kXH).
+  auto cycle = [&](int st0, auto tail_tag, auto head_tag) {
+    constexpr bool kTail = decltype(tail_tag)::value, kHead = decltype(head_tag)::value;
+    static_assert(!(kTail && kHead), "a tile has at least two cycles");
+#pragma unroll
+    for (int u = 0; u < kWB; ++u) {
+      const int sa = st0 + u + kWA, sb = st0 + u + kWB;   // past the end exactly in the tail
+      const int wslot = aslot == 0 ? kWAS - 1 : aslot - 1;
+      dma_a(wslot, kTail, kTail ? sa - nk : sa);
+      wait_b(u, kHead);                    // weight stage u: before the epilogue
+      to_region(u);
+      load_b(u, kTail, kTail ? sb - nk : sb);
+      multiply(aslot);
+      stage_end(kHead && u + 1 < kWB);     // A stage u + 1: before the epilogue for u + 1 < kWB
+      aslot = aslot == kWAS - 1 ? 0 : aslot + 1;
+    }
+  };
+  for (int j = 0; j < ntile; ++j) {
+    cycle(0, std::false_type{}, std::true_type{});
+    for (int st0 = kWB; st0 < nk - kWB; st0 += kWB) cycle(st0, std::false_type{}, std::false_type{});
+    a_offsets(a_off_nxt, pv_nxt, nxt);
+    cycle(nk - kWB, std::true_type{}, std::false_type{});
+    epilogue(cur);
+    zero_acc();
+    cur = nxt;
+    nxt = tile(min(j + 2, ntile - 1));
+#pragma unroll
+    for (int q = 0; q < kPLoads; ++q) a_off_cur[q] = a_off_nxt[q];
+    fetch_perm(pv_nxt, nxt);
+  }
+  wait_vmcnt<0>();
+}
+
 // ---------------------------------------------------------------- combine
 // One wave per token; lane owns 8 columns per 512-column chunk.  The GEMMs leave each
 // assignment's expert output and the shared expert's output unscaled (bf16 of the fp32
@@ -1021,6 +1348,12 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   if (!n_cu[dev] && hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return TMOE_ERR_HIP;
   const unsigned pgrid = (unsigned)(n_cu[dev] >= 8 ? n_cu[dev] / 8 * 8 : 8);
+  // bf16 groups of the persistent shapes run on the whole-line kernel; TMOE_PREFILL_GEMM=frag
+  // selects the fragment-load kernel for them (int4 groups always use it).
+  static const bool frag = [] {
+    const char* e = getenv("TMOE_PREFILL_GEMM");
+    return e && !strcmp(e, "frag");
+  }();
   auto gemm = [&](GemmParams g, int lo, int hi, bool routed_q4, long mchunks) {
     g.group_lo = lo;
     g.group_hi = hi;
@@ -1029,6 +1362,10 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
       hipLaunchKernelGGL((k_grouped_gemm_p<true, true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent && routed_q4)
       hipLaunchKernelGGL((k_grouped_gemm_p<true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (persistent && !frag && g.up)
+      hipLaunchKernelGGL(k_grouped_gemm_w<true>, dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (persistent && !frag)
+      hipLaunchKernelGGL(k_grouped_gemm_w<false>, dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent)
       hipLaunchKernelGGL((k_grouped_gemm_p<false>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (routed_q4 && qr)
@@ -1043,6 +1380,7 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   up.T = T; up.E = E; up.k = k; up.n_groups = n_groups; up.n_ntiles = I / up_cols; up.up = 1; up.N = I; up.I = I;
   up.table = table; up.shw0 = sh_gate; up.shw1 = sh_up; up.shared_row0 = T * k; up.out = act;
   up.desc = desc;
+  up.sink = reinterpret_cast<uint16_t*>(tile_start + ((E + 5) & ~3));   // past tile_start's E + 2 words
   GemmParams dn = up;
   dn.a = act; dn.K = I; dn.gather = 0; dn.n_ntiles = H / dn_cols; dn.up = 0; dn.N = H;
   dn.shw0 = sh_down; dn.shw1 = nullptr; dn.out = ch; dn.out_sh = sh;

@@ -180,5 +180,17 @@ __device__ __forceinline__ float sigmoid_f32(float z) { return 1.0f / (1.0f + ex
 // SwiGLU activation at the reference's bf16 rounding points:
 // bf16(bf16(silu(g)) * u) with g, u already bf16 values.
 __device__ __forceinline__ float swiglu_bf16(float g, float u) { return rbf16(rbf16(silu_f32(g)) * u); }
+// The same rounding points from two fp32 accumulators, as bf16 bits: the conversions are
+// the hardware's (v_cvt_pk_bf16_f32, round to nearest even like f32_to_bf16 for every value
+// but NaN payloads) and silu is g * rcp(1 + e^-g) (the hardware reciprocal, within ~1 ulp of
+// fp32 g / (1 + e^-g)).  The prefill GEMM epilogue's form, where an IEEE division and
+// software rounding would hold up the weight stream.
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t swiglu_bits_hw(float gacc, float uacc) {
+  const uint32_t gu = __builtin_bit_cast(uint32_t, bf16x2_hw{(__bf16)gacc, (__bf16)uacc});
+  const float g = __uint_as_float(gu << 16), u = __uint_as_float(gu & 0xFFFF0000u);
+  const float s = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + expf(-g)));
+  return __builtin_bit_cast(uint16_t, (__bf16)(s * u));
+}
 
 }  // namespace tmoe
