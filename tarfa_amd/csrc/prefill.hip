@@ -903,19 +903,18 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 // request weight stage g + kWB into them; 40 MFMAs; wait for A stage g + 1; barrier.
 // K: a multiple of 4 stages (256) and at least 8 stages (the next tile's perm words, requested
 // after a tile's epilogue, are used before its last cycle, 4 stage waits later).
-constexpr int kWB = 4;                        // weight stages in registers (the unrolled cycle)
-constexpr int kWAS = 5;                       // A ring slots
-constexpr int kWA = kWAS - 1;                 // A stages requested ahead (= kWB: every request
-                                              // past a tile's end falls in its last cycle)
+// WB: weight stages in registers (the unrolled cycle; 4, or 5 where K / 64 is a multiple of
+// 5), A stages requested as far ahead (every request past a tile's end falls in its last
+// cycle), WB + 1 A ring slots.
 constexpr int kWBLoads = 2 * kPNB;            // weight loads per wave per stage (8 rows each)
 constexpr int kWReg = 16 * kPNB * 8;          // u32x4 per wave region (32 rows x 128 B)
 constexpr int kWOps = kPLoads + kWBLoads;     // vector memory operations per stage
-static_assert(kWA == kWB, "A and weight stages requested equally far ahead");
-static_assert(kWBLoads + (kWA - 1) * kWOps < 64 && (kWB - 1) * kWOps + kPLoads < 64, "vmcnt range");
-static_assert((kWAS * kPSlot + kPW * kWReg) * 16 <= 160 * 1024, "LDS");
 
-template <bool UP>
+template <bool UP, int WB>
 __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
+  constexpr int kWB = WB, kWA = WB, kWAS = WB + 1;
+  static_assert(kWBLoads + (kWA - 1) * kWOps < 64 && (kWB - 1) * kWOps + kPLoads < 64, "vmcnt range");
+  static_assert((kWAS * kPSlot + kPW * kWReg) * 16 <= 160 * 1024, "LDS");
   __shared__ u32x4 lA[kWAS * kPSlot];
   __shared__ u32x4 lB[kPW * kWReg];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1362,10 +1361,12 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
       hipLaunchKernelGGL((k_grouped_gemm_p<true, true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent && routed_q4)
       hipLaunchKernelGGL((k_grouped_gemm_p<true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    else if (persistent && !frag && g.up && g.K % (5 * kBK) == 0)
+      hipLaunchKernelGGL((k_grouped_gemm_w<true, 5>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent && !frag && g.up)
-      hipLaunchKernelGGL(k_grouped_gemm_w<true>, dim3(pgrid), dim3(64 * kPW), 0, s, g);
+      hipLaunchKernelGGL((k_grouped_gemm_w<true, 4>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent && !frag)
-      hipLaunchKernelGGL(k_grouped_gemm_w<false>, dim3(pgrid), dim3(64 * kPW), 0, s, g);
+      hipLaunchKernelGGL((k_grouped_gemm_w<false, 4>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (persistent)
       hipLaunchKernelGGL((k_grouped_gemm_p<false>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
     else if (routed_q4 && qr)
