@@ -319,7 +319,7 @@ def run(args, log):
                             "expert bf16): routed weights dequantised in registers into the MFMA fragments",
                 "us_per_layer": round(pus4, 1), "tflops": round(prefill_flops(shape, T4) / (pus4 * 1e-6) / 1e12, 1),
                 "weight_bytes": wb4, "weight_gbps": round(wb4 / (pus4 * 1e-6) / 1e9, 1),
-                "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_p_prefill_t4096_h2560_e256_i1024_k8.md",
+                "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_w_prefill_t4096_h2560_e256_i1024_k8.md",
                                                             "int4_traffic_bytes_per_launch")}
             log(f"int4 prefill: {pus4:.1f} us/layer")
             del pws4, px4, plg4
@@ -357,7 +357,7 @@ def run(args, log):
                              "weight_gbps": round(wgbs, 1), "hbm_frac": round(wgbs / HBM_PEAK_GBS, 4),
                              "attainable_tflops": round(attain, 1), "roofline_frac": round(tflops / attain, 4),
                              "flops": fl, "weight_bytes": wb, "tokens_per_s": round(T / (pus * 1e-6), 1),
-                             "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_p_prefill_t4096_h2560_e256_i1024_k8.md")}
+                             "gemm_traffic_per_launch": profiled_traffic("k_grouped_gemm_w_prefill_t4096_h2560_e256_i1024_k8.md")}
         log(f"prefill: {pus:.1f} us/layer, {tflops:.1f} TFLOP/s, weights {wgbs:.0f} GB/s")
         del pws, px, plg
 
