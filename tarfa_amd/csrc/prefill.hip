@@ -1063,13 +1063,21 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
       bf16x8_t b[kPNB];
 #pragma unroll
       for (int nb = 0; nb < kPNB; ++nb) b[nb] = as_bf16x8(reg[nb * 128 + rd]);
+      auto blocks = [&](int i0, int i1) {
 #pragma unroll
-      for (int i = 0; i < kPMB; ++i) {
-        const bf16x8_t a = as_bf16x8(la[i * 128 + rd]);
+        for (int i = i0; i < i1; ++i) {
+          const bf16x8_t a = as_bf16x8(la[i * 128 + rd]);
 #pragma unroll
-        for (int nb = 0; nb < kPNB; ++nb)
-          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[i][nb], 0, 0, 0);
-      }
+          for (int nb = 0; nb < kPNB; ++nb)
+            acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[i][nb], 0, 0, 0);
+        }
+      };
+      // Down: chunks of at most 128 rows (about half the groups at ~128 tokens per expert)
+      // skip the last two row blocks, all padding (down 387 -> 369 us at T=4096; the up
+      // GEMM showed no gain and keeps one straight-line schedule).
+      static_assert(kPMB == 10, "8 row blocks, then the two that chunks over 128 rows use");
+      blocks(0, 8);
+      if (UP || cur.m > 128) blocks(8, kPMB);
     }
   };
   auto barrier_raw = [&]() {
