@@ -228,7 +228,7 @@ def run(args, log):
     result = {
         "metric": METRIC, "value": round(us, 3), "unit": "us/token-layer", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic: seeded counter-based generator, weights ~N(0,0.02), x ~N(0,1)",
+        "dtype": "bf16", "data": "synthetic: seeded counter-based generator (sum of twelve uniforms), weights ~N(0,0.02), x ~N(0,1)",
         "config": {"workload": "full-size exact-BF16 MoE decode layer, batch 1 (router + 8 routed SwiGLU experts "
                                "+ shared expert + combine)",
                    "hidden": H, "experts": shape.num_experts, "intermediate": shape.intermediate,

@@ -8,7 +8,7 @@ anything here and fails loudly when its HIP library is missing.
 Modules
 -------
 bf16    IEEE round-to-nearest-even fp32 -> bf16 on uint32 bit patterns.
-rng     counter-based seeded generator (splitmix64 finaliser, Irwin-Hall normal
+rng     counter-based seeded generator (splitmix64 finaliser, Irwin-Hall n=12 normal
         approximation) whose device twin is ``tarfa_amd/csrc/fill.hip``.
 moe     router (fp32 logits, softmax, top-k, renorm), dispatch permutation,
         exact-BF16 expert SwiGLU for decode and prefill, shared expert, combine.

@@ -10,15 +10,16 @@ regenerate any single expert it needs.
 
 * hash  : splitmix64 output function (S. Vigna, "splitmix64.c", 2015, public
           domain): ``h_i = mix(key + (i + 1) * 0x9E3779B97F4A7C15)``.
-* normal: Irwin-Hall sum of four uniforms, centred and scaled to unit variance.
-  - ``n16``: four 16-bit fields of one hash; the integer sum is exact, converted
-    to fp32 exactly and multiplied once by an fp32 constant (one IEEE rounding),
-    then rounded to bf16.  Used for bf16 weights and activations.
-  - ``n32``: four 32-bit fields of two hashes, summed exactly in int64, scaled in
-    fp64 and rounded once to fp32.  Used for fp32 router logits, where the
-    finer grid keeps exact ties out of the top-9.
-  The distribution is bounded at +-3.46 sigma (Irwin-Hall n=4); it stands in for
-  the reference's ``~N(0, sigma)``.
+* normal: Irwin-Hall sum of twelve uniforms (the classical sum-of-twelve normal
+  approximation), centred and scaled to unit variance.
+  - ``n16``: the twelve 16-bit fields of hashes 3i, 3i+1, 3i+2; the integer sum is
+    exact, converted to fp32 exactly and multiplied once by an fp32 constant (one
+    IEEE rounding), then rounded to bf16.  Used for bf16 weights and activations.
+  - ``n32``: the twelve 32-bit fields of hashes 6i .. 6i+5, summed exactly in int64,
+    scaled in fp64 and rounded once to fp32.  Used for fp32 router logits, where
+    the finer grid keeps exact ties out of the top-9.
+  It stands in for the reference's ``~N(0, sigma)``: bounded at +-6 sigma, excess
+  kurtosis -0.1, P(|z| > 3) = 0.20% (the normal's: 0.27%; four uniforms: 0.04%).
 """
 import math
 
@@ -28,8 +29,10 @@ from . import bf16
 
 GOLDEN = 0x9E3779B97F4A7C15
 M64 = (1 << 64) - 1
-STD16 = math.sqrt((65536.0 ** 2 - 1.0) / 3.0)   # std of a sum of four U{0..65535}
-STD32 = math.sqrt((2.0 ** 64 - 1.0) / 3.0)      # std of a sum of four U{0..2^32-1}
+STD16 = math.sqrt(65536.0 ** 2 - 1.0)   # std of a sum of twelve U{0..65535}
+STD32 = math.sqrt(2.0 ** 64 - 1.0)      # std of a sum of twelve U{0..2^32-1}
+MID16 = 12 * 65535 // 2                 # mean of that sum (an integer)
+MID32 = 6 * 0xFFFFFFFF
 
 # tensor kinds in a stream id: (layer << 40) | (kind << 32) | expert
 KIND_GATE_UP, KIND_DOWN, KIND_ROUTER, KIND_SH_GATE, KIND_SH_UP, KIND_SH_DOWN, \
@@ -71,10 +74,13 @@ def scale16(std):
 
 
 def n16_f32(k, n, std, start=0):
-    h = hashes(k, start, n)
+    h = hashes(k, 3 * start, 3 * n).reshape(n, 3)
     m = np.uint64(0xFFFF)
-    s = (h & m) + ((h >> np.uint64(16)) & m) + ((h >> np.uint64(32)) & m) + (h >> np.uint64(48))
-    c = s.astype(np.int64) - 131070
+    s = np.zeros(n, dtype=np.uint64)
+    for j in range(3):
+        hj = h[:, j]
+        s += (hj & m) + ((hj >> np.uint64(16)) & m) + ((hj >> np.uint64(32)) & m) + (hj >> np.uint64(48))
+    c = s.astype(np.int64) - MID16
     return c.astype(np.float32) * scale16(std)
 
 
@@ -84,13 +90,14 @@ def n16_bf16_bits(k, n, std, start=0):
 
 
 def n32_f32(k, n, std, start=0):
-    """fp32 normals from two hashes per element (hash indices 2i and 2i+1)."""
-    h = hashes(k, 2 * start, 2 * n)
-    lo, hi = h[0::2], h[1::2]
+    """fp32 normals from six hashes per element (hash indices 6i .. 6i+5)."""
+    h = hashes(k, 6 * start, 6 * n).reshape(n, 6)
     m = np.uint64(0xFFFFFFFF)
-    s = ((lo & m).astype(np.int64) + (lo >> np.uint64(32)).astype(np.int64)
-         + (hi & m).astype(np.int64) + (hi >> np.uint64(32)).astype(np.int64))
-    c = s - 2 * 0xFFFFFFFF
+    s = np.zeros(n, dtype=np.int64)
+    for j in range(6):
+        hj = h[:, j]
+        s += (hj & m).astype(np.int64) + (hj >> np.uint64(32)).astype(np.int64)
+    c = s - MID32
     return (c.astype(np.float64) * (std / STD32)).astype(np.float32)
 
 

@@ -2,10 +2,11 @@
 //
 // Element i of a tensor with key K is a pure function of (K, start + i):
 //   h_i = mix(K + (i + 1) * 0x9E3779B97F4A7C15)       splitmix64 output function
-//   bf16: c = sum of the four 16-bit fields of h_i - 131070 (exact int),
+//   bf16: c = sum of the twelve 16-bit fields of h_{3i}, h_{3i+1}, h_{3i+2} - 393210 (exact int),
 //         value = bf16(fp32(c) * scale)                 one fp32 rounding, then RNE
-//   fp32: c = sum of the four 32-bit fields of h_{2i}, h_{2i+1} - 2*(2^32-1) (exact int64),
+//   fp32: c = sum of the twelve 32-bit fields of h_{6i} .. h_{6i+5} - 6*(2^32-1) (exact int64),
 //         value = fp32(double(c) * scale)               one fp64 rounding, then RNE to fp32
+// (Irwin-Hall n = 12: the classical sum-of-twelve-uniforms normal, bounded at +-6 sigma.)
 // Integer sums, int->float conversions of exactly representable integers and
 // single IEEE multiplies round identically on host and device, so the host can
 // regenerate any slab bit-for-bit.  The whole-model weight set (~194 GB at
@@ -31,8 +32,13 @@ __global__ __launch_bounds__(256) void k_fill_bf16(uint16_t* __restrict__ dst, u
     uint16_t v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint64_t h = hash_at(key, start + base + j);
-      const int32_t c = (int32_t)((h & 0xFFFF) + ((h >> 16) & 0xFFFF) + ((h >> 32) & 0xFFFF) + (h >> 48)) - 131070;
+      const uint64_t i3 = 3ull * (start + base + j);
+      int32_t c = -393210;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const uint64_t h = hash_at(key, i3 + q);
+        c += (int32_t)((h & 0xFFFF) + ((h >> 16) & 0xFFFF) + ((h >> 32) & 0xFFFF) + (h >> 48));
+      }
       v[j] = f32_to_bf16((float)c * scale);
     }
     if (base + 8 <= n && (((uintptr_t)(dst + base)) & 15) == 0) {
@@ -52,10 +58,12 @@ __global__ __launch_bounds__(256) void k_fill_f32(float* __restrict__ dst, uint6
                                                   uint64_t start) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const uint64_t lo = hash_at(key, 2ull * (start + i)), hi = hash_at(key, 2ull * (start + i) + 1ull);
-    const int64_t s = (int64_t)(lo & 0xFFFFFFFFull) + (int64_t)(lo >> 32) + (int64_t)(hi & 0xFFFFFFFFull) +
-                      (int64_t)(hi >> 32);
-    const int64_t c = s - 2ll * 0xFFFFFFFFll;
+    int64_t c = -6ll * 0xFFFFFFFFll;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const uint64_t h = hash_at(key, 6ull * (start + i) + q);
+      c += (int64_t)(h & 0xFFFFFFFFull) + (int64_t)(h >> 32);
+    }
     dst[i] = (float)((double)c * scale);
   }
 }

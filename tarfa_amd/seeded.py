@@ -2,7 +2,7 @@
 
 Every tensor element is a pure function of (seed, stream, index) computed by the
 ``tmoe_fill_*`` kernels (splitmix64 output function over ``key + (i+1) * golden``,
-Irwin-Hall n=4 normal), so a full-size model (48 x 256 experts) is written
+Irwin-Hall n=12 normal), so a full-size model (48 x 256 experts) is written
 straight into HBM and any single expert can be regenerated on the host.
 
 A stream id is ``(layer << 40) | (kind << 32) | expert``.
@@ -14,8 +14,8 @@ import torch
 
 GOLDEN = 0x9E3779B97F4A7C15
 M64 = (1 << 64) - 1
-STD16 = math.sqrt((65536.0 ** 2 - 1.0) / 3.0)
-STD32 = math.sqrt((2.0 ** 64 - 1.0) / 3.0)
+STD16 = math.sqrt(65536.0 ** 2 - 1.0)   # std of a sum of twelve U{0..65535}
+STD32 = math.sqrt(2.0 ** 64 - 1.0)      # std of a sum of twelve U{0..2^32-1}
 
 KIND_GATE_UP, KIND_DOWN, KIND_ROUTER, KIND_SH_GATE, KIND_SH_UP, KIND_SH_DOWN, \
     KIND_SH_GATEW, KIND_X, KIND_LOGITS = range(9)

@@ -60,12 +60,18 @@ def test_generator_vectorised_equals_bigint():
     h = rng.hashes(k, 1000, 64)
     for i in range(64):
         assert int(h[i]) == rng._mix_int(k + (1000 + i + 1) * rng.GOLDEN)
-    # n16: the centred sum of four 16-bit fields, times one fp32 constant
+    # n16: the centred sum of the twelve 16-bit fields of hashes 3i .. 3i+2, times one fp32 constant
     z = rng.n16_f32(k, 64, 0.02, start=1000)
     for i in range(64):
-        v = int(h[i])
-        c = sum((v >> s) & 0xFFFF for s in (0, 16, 32, 48)) - 131070
+        c = sum((rng._mix_int(k + (3 * (1000 + i) + j + 1) * rng.GOLDEN) >> s) & 0xFFFF
+                for j in range(3) for s in (0, 16, 32, 48)) - 393210
         assert z[i] == np.float32(np.float32(c) * rng.scale16(0.02))
+    # n32: the twelve 32-bit fields of hashes 6i .. 6i+5, in fp64, rounded once to fp32
+    y = rng.n32_f32(k, 16, 1.0, start=77)
+    for i in range(16):
+        c = sum((rng._mix_int(k + (6 * (77 + i) + j + 1) * rng.GOLDEN) >> s) & 0xFFFFFFFF
+                for j in range(6) for s in (0, 32)) - 6 * 0xFFFFFFFF
+        assert y[i] == np.float32(c * (1.0 / rng.STD32))
 
 
 def test_generator_moments_and_determinism():
@@ -79,6 +85,21 @@ def test_generator_moments_and_determinism():
     # distinct streams are uncorrelated
     c = rng.n16_f32(rng.key(7, rng.stream_id(rng.KIND_GATE_UP, 0, 2)), 1 << 20, 1.0)
     assert abs(np.corrcoef(a, c)[0, 1]) < 5e-3
+
+
+def test_generator_tails_are_close_to_normal():
+    """Irwin-Hall n=12: excess kurtosis -1.2/12 = -0.1 and P(|z| > 3) = 0.002014 (the
+    closed-form CDF of a sum of twelve uniforms), against 0 and 0.002700 for N(0, 1); |z| <= 6.
+    The n=4 form (kurtosis -0.3, P(|z| > 3) = 0.00043, |z| <= 3.46) fails these bounds."""
+    k = rng.key(9, rng.stream_id(rng.KIND_X, 0, 0))
+    a = rng.n16_f32(k, 1 << 22, 1.0).astype(np.float64)
+    kurt = np.mean(a ** 4) / np.mean(a ** 2) ** 2 - 3.0
+    assert abs(kurt - (-0.1)) < 0.01
+    tail = np.mean(np.abs(a) > 3.0)
+    assert 0.0019 < tail < 0.00215
+    assert np.abs(a).max() <= 6.0 + 1e-3
+    b = rng.n32_f32(k, 1 << 20, 1.0).astype(np.float64)
+    assert abs(np.mean(b ** 4) / np.mean(b ** 2) ** 2 - 3.0 - (-0.1)) < 0.02
 
 
 # ------------------------------------------------------------------ router
