@@ -25,8 +25,9 @@
 // column tile's last down block) never go through an agent-scope release fence: that writes
 // back the XCD's whole L2, and hundreds of them serialise (measured: ~140 us instead of ~20
 // for the down kernel).  The data are written with agent-scope atomic stores, which write
-// through to memory; each wave waits for its stores to complete (a workgroup-scope release,
-// s_waitcnt) before the block's arrival is counted with an agent-scope atomic; the last
+// through to memory; each wave waits for its stores to complete (s_waitcnt vmcnt(0): a
+// workgroup-scope release fence only waits for LDS) before the block's arrival is counted
+// with an agent-scope atomic; the last
 // block reads the data with agent-scope atomic loads, which miss in its own L2.
 //
 // Groups and slices.  Every up block derives the groups from the T*k ids in LDS: the experts
@@ -109,6 +110,11 @@ struct SbGroups {
 __device__ __forceinline__ int sb_load_id(const SbParams& p, int j) {
   return p.ids32 ? p.ids32[j] : (int)p.ids64[j];
 }
+
+// This wave's stores have completed (vmcnt(0)).  The hand-off stores are device-scope
+// (write-through), so once complete they are visible to device-scope loads; a workgroup-scope
+// release fence would not do: it compiles to an LDS wait only.
+__device__ __forceinline__ void sb_stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ int sb_group_of(const SbGroups& g, int e) {
   return g.wpre[e >> 5] + __popc(g.present[e >> 5] & ((1u << (e & 31)) - 1u));
@@ -564,7 +570,7 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
   }
   // Arrival on the 64-column combine tile once the stores have completed; the last of its
   // 2 x (slices) waves combines it and re-zeroes the counter.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  sb_stores_done();
   const int ct = tile >> 1;
   const uint32_t arrivals = 2u * (uint32_t)total;
   uint32_t prev = 0;
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(256) void k_sb_router(const uint16_t* __restrict__ 
         if (e0 + r < E) __hip_atomic_store(lt + e0 + r, d[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  sb_stores_done();
   __syncthreads();
   if (threadIdx.x == 0)
     last = __hip_atomic_fetch_add(cnt + t * kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
