@@ -46,7 +46,6 @@
 // (row r, column c) at ((c / 8) * m + r) * 8 + c % 8, so lane (r, q) of an MFMA reads its 8
 // k-values as one 16-byte word, and a wave's part of K is one contiguous run.
 #include "tmoe_gemv.h"
-#include "tmoe_topk.h"
 #include "tmoe_ws.h"
 
 namespace tmoe {
@@ -583,45 +582,6 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
   if (lane == 0) __hip_atomic_store(p.cnt + ct * kLine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Top-k of one token's E <= 256 logits (4 per lane), k <= 8, by one wave: the bitonic
-// selection of tmoe_topk.h (lane r < k gets slot r), then the softmax and renormalisation of
-// wave_topk_values with the same operations in the same order (the denominator a wave sum,
-// the renormalising sum over slots 0 .. k-1 in order), so ids and weights are bit-identical
-// to it; lane r writes slot r.
-__device__ __forceinline__ void sb_topk8(const float* lt, int E, int k, int lane, const TopkOut& o) {
-  float v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e < E ? __hip_atomic_load(lt + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-  }
-  int id = E;
-  float lw = -INFINITY, top = 0.f;
-  top8_bitonic(v, E, k, lane, id, lw, top);
-  // The largest logit (slot 0's), -inf when nothing is selectable.
-  const bool any = __builtin_amdgcn_readfirstlane(id) != E;
-  const float m0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(any ? lw : -INFINITY)));
-  float ls = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (lane + 64 * i < E) ls += expf(v[i] - m0);
-  const float S = wave_sum(ls);
-  const bool mine = lane < k && id != E;
-  const float pr = mine ? expf(lw - m0) / S : 0.f;
-  float psum = 0.f;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) psum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), r));
-  const float w = mine ? rbf16(pr / psum) : 0.f;
-  if (lane < k) {
-    const uint16_t wb = f32_to_bf16(w);
-    if (o.ids32) o.ids32[lane] = id;
-    if (o.wf) o.wf[lane] = w;
-    if (o.ids64) o.ids64[lane] = id;
-    if (o.wb) o.wb[lane] = wb;
-    if (o.heat && id < E) atomicAdd(o.heat + id, 1u);
-  }
-}
-
 // Router logits and per-token top-k.  Block (t, y): wave w computes logits 16 y + 4 w .. + 3
 // of token t and stores them with agent-scope atomic stores; the token's last block selects.
 template <int MAXC, int MAXEPL>
@@ -658,8 +618,7 @@ __global__ __launch_bounds__(256) void k_sb_router(const uint16_t* __restrict__ 
     o.wf += (size_t)t * k;
     if (o.ids64) o.ids64 += (size_t)t * k;
     if (o.wb) o.wb += (size_t)t * k;
-    if (MAXEPL == 4 && k <= 8) sb_topk8(lt, E, k, lane, o);
-    else wave_topk<MAXEPL>(lt, true, E, k, lane, o);
+    wave_topk<MAXEPL>(lt, true, E, k, lane, o);
   } else if (threadIdx.x == 64) {
     __hip_atomic_store(cnt + t * kLine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }

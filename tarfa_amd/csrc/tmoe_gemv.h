@@ -5,6 +5,7 @@
 #include <math.h>
 
 #include "tmoe_device.h"
+#include "tmoe_topk.h"
 
 namespace tmoe {
 
@@ -243,8 +244,51 @@ __device__ __forceinline__ void wave_topk_select(const float* src, int E, int k,
   wave_topk_values<MAXEPL, MAXK>(v, E, k, lane, id, w);
 }
 
+// E <= 256 logits (4 per lane), k <= 8: the bitonic selection of tmoe_topk.h (lane r < k
+// gets slot r), then the softmax and renormalisation of wave_topk_values with the same
+// operations in the same order (the denominator a wave sum, the renormalising sum over
+// slots 0 .. k-1 in order), so ids and weights are bit-identical to the k-round selection;
+// lane r writes slot r.
+__device__ __forceinline__ void wave_topk8(const float* src, bool coherent, int E, int k, int lane,
+                                           const TopkOut& o) {
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e >= E ? -INFINITY : coherent ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                         : src[e];
+  }
+  int id = E;
+  float lw = -INFINITY, top = 0.f;
+  top8_bitonic(v, E, k, lane, id, lw, top);
+  // The largest logit (slot 0's), -inf when nothing is selectable.
+  const bool any = __builtin_amdgcn_readfirstlane(id) != E;
+  const float m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(any ? lw : -INFINITY)));
+  float ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (lane + 64 * i < E) ls += expf(v[i] - m);
+  const float S = wave_sum(ls);
+  const bool mine = lane < k && id != E;
+  const float pr = mine ? expf(lw - m) / S : 0.f;
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) psum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), r));
+  const float w = mine ? rbf16(pr / psum) : 0.f;
+  if (lane < k) {
+    if (o.ids32) o.ids32[lane] = id;
+    if (o.wf) o.wf[lane] = w;
+    if (o.ids64) o.ids64[lane] = id;
+    if (o.wb) o.wb[lane] = f32_to_bf16(w);
+    if (o.heat && id < E) atomicAdd(o.heat + id, 1u);
+  }
+}
+
 template <int MAXEPL>
 __device__ __forceinline__ void wave_topk(const float* src, bool coherent, int E, int k, int lane, const TopkOut& o) {
+  if constexpr (MAXEPL == 4) {
+    if (k <= 8) return wave_topk8(src, coherent, E, k, lane, o);
+  }
   int id[16];
   float w[16];
   if (coherent) {
