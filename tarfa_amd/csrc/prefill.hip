@@ -1032,7 +1032,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
   // Wait for weight stage bs (requested kWB - 1 iterations and one A group before, plus X
   // operations of an epilogue in between).  The registers pass through the asm, so nothing
   // reads them before the wait.
-  // Stores per thread in one epilogue (up: 2 passes x 3, down: 5 passes x 2); the first 4
+  // Stores per thread in one epilogue (up: 2 passes x 3, down: 2 passes x 5); the first 4
   // iterations of the next tile add them and the next tile's perm loads (kXH) to their waits.
   constexpr int kEpiStores = UP ? 6 : 10;
   constexpr int kXH = kEpiStores + kPLoads;
@@ -1096,24 +1096,30 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
     barrier_raw();
   };
 
-  // Epilogue through the wave regions (32 KB, free between a tile's last stage and the next
-  // tile's first), as in k_grouped_gemm_p: passes of BPP 16-row blocks, row r's 16-byte chunk
-  // q at chunk q ^ 2 ((r / 4) % 4); C fragment lane l holds rows 4 (l / 16) + e, column l % 16.
-  auto epilogue = [&](const PTile& t) {
+  // Epilogue in two passes of five 16-row blocks, row r's 16-byte chunk q at chunk
+  // q ^ 2 ((r / 4) % 4); C fragment lane l holds rows 4 (l / 16) + e, column l % 16.
+  // Staging: the wave regions (32 KB, free between a tile's last stage and the next tile's
+  // first) hold the pass's first kStgRows rows, the A ring slot
+  // that no load targets during the epilogue (the one the tile's last stage used; its refill
+  // is requested in the next tile's first iteration) the rest.
+  auto epilogue = [&](const PTile& t, int free_slot) {
     constexpr int TCB = UP ? 2 * kPUpCols : 2 * kPDnCols;
-    constexpr int BPP = UP ? 5 : 2;
+    constexpr int BPP = 5;
     constexpr int RPP = 16 * BPP, CPR = TCB / 16;
     constexpr int NST = (RPP * CPR + 64 * kPW - 1) / (64 * kPW);
-    static_assert(RPP * TCB <= kPW * kWReg * 16 && kPMB % BPP == 0, "a pass fits in the regions");
-    static_assert(NST * 64 * kPW / CPR * TCB <= kPW * kWReg * 16, "reads past the pass stay in the regions");
+    constexpr int kStgRows = kPW * kWReg * 16 / TCB;
+    static_assert(kPMB % BPP == 0 && RPP <= kStgRows + kPSlot * 16 / TCB, "a pass fits in the staging");
+    static_assert(NST * 64 * kPW / CPR <= kStgRows + kPSlot * 16 / TCB, "reads past the pass stay in it");
     static_assert(NST * (kPMB / BPP) == kEpiStores, "stores per thread per epilogue");
-    char* stg = reinterpret_cast<char*>(lB);
+    char* const stg = reinterpret_cast<char*>(lB);
+    char* const stg2 = reinterpret_cast<char*>(lA + free_slot * kPSlot);
+    auto rowp = [&](int r) { return r < kStgRows ? stg + r * TCB : stg2 + (r - kStgRows) * TCB; };
     const int sw = 2 * (lane >> 4), rl = 4 * (lane >> 4);
     int cb[kPNB];
 #pragma unroll
     for (int nb = 0; nb < kPNB; ++nb) {
       const int col = UP ? wid * 16 + lrow : wid * 32 + nb * 16 + lrow;
-      cb[nb] = rl * TCB + ((col >> 3) ^ sw) * 16 + (col & 7) * 2;
+      cb[nb] = ((col >> 3) ^ sw) * 16 + (col & 7) * 2;
     }
 #pragma unroll
     for (int P = 0; P < kPMB / BPP; ++P) {
@@ -1123,14 +1129,15 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
         if (16 * i >= t.m) continue;   // padding rows only (their stores go to the sink)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          char* rowp = stg + (ii * 16 + e) * TCB;
+          char* const row = rowp(ii * 16 + rl + e);
           if constexpr (UP) {
-            *reinterpret_cast<uint16_t*>(rowp + cb[0]) =
-                swiglu_bits_hw(acc[i][0][e], acc[i][1][e]);
+            *reinterpret_cast<uint16_t*>(row + cb[0]) = swiglu_bits_hw(acc[i][0][e], acc[i][1][e]);
           } else {
-#pragma unroll
-            for (int nb = 0; nb < kPNB; ++nb)
-              *reinterpret_cast<uint16_t*>(rowp + cb[nb]) = f32_to_bf16(acc[i][nb][e]);
+            // both columns' values in one hardware conversion (round to nearest even)
+            static_assert(kPNB == 2, "two column blocks per wave");
+            const uint32_t pk = __builtin_bit_cast(uint32_t, bf16x2_hw{(__bf16)acc[i][0][e], (__bf16)acc[i][1][e]});
+            *reinterpret_cast<uint16_t*>(row + cb[0]) = (uint16_t)pk;
+            *reinterpret_cast<uint16_t*>(row + cb[1]) = (uint16_t)(pk >> 16);
           }
         }
       }
@@ -1142,7 +1149,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
       for (int q = 0; q < NST; ++q) {
         const int x = tid + q * 64 * kPW;
         const int rr = x / CPR, qc = x - rr * CPR, row = P * RPP + rr;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * TCB + ((qc ^ (2 * ((rr >> 2) & 3))) * 16));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(rowp(rr) + ((qc ^ (2 * ((rr >> 2) & 3))) * 16));
         const bool ok = x < RPP * CPR && row < t.m;
         *reinterpret_cast<u32x4*>(ok ? t.o + (size_t)row * p.N + qc * 8 : p.sink) = v;
       }
@@ -1200,7 +1207,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_w(GemmParams p) {
     for (int st0 = kWB; st0 < nk - kWB; st0 += kWB) cycle(st0, std::false_type{}, std::false_type{});
     a_offsets(a_off_nxt, pv_nxt, nxt);
     cycle(nk - kWB, std::true_type{}, std::false_type{});
-    epilogue(cur);
+    epilogue(cur, aslot == 0 ? kWAS - 1 : aslot - 1);
     zero_acc();
     cur = nxt;
     nxt = tile(min(j + 2, ntile - 1));
