@@ -780,12 +780,16 @@ struct TaskRef {
 
 
 // Task t of the list R, then per slot j: Gj, D(j - kDownLag) once j >= kDownLag,
-// S after G(sh_after) and SD after G(sd_after); then the remaining D.  Pure arithmetic on values
-// held in scalar registers: a lookup table in kernel-argument memory costs a
-// memory round trip per step.
+// S after G(sh_after) (right after R when sh_after < 0) and SD after G(sd_after); then the
+// remaining D.  Pure arithmetic on values held in scalar registers: a lookup table in
+// kernel-argument memory costs a memory round trip per step.
 __device__ __forceinline__ TaskRef decode_task(const DecodeParams& p, int t) {
   if (t < p.n_r) return {kTR, 0, t};
   t -= p.n_r;
+  if (p.sh_after < 0) {
+    if (t < p.n_s) return {kTS, 0, t};
+    t -= p.n_s;
+  }
   for (int j = 0; j < p.k; ++j) {
     if (t < p.n_g) return {kTG, j, t};
     t -= p.n_g;
@@ -958,7 +962,8 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       route_fetch(p, lane, rwc, tag, err, s_rt);
       routed = true;
       if (p.trace) ts_route = __builtin_amdgcn_s_memrealtime();
-      if (t == p.n_r) publish_routing(p, lane, rwc);   // task n_r: the first gate/up task of slot 0
+      // The first gate/up task of slot 0 publishes (after R, and after S when S leads).
+      if (t == p.n_r + (p.sh_after < 0 ? p.n_s : 0)) publish_routing(p, lane, rwc);
     }
     if (tk.type == kTR) {
       task_router<MH, EXACT, LN>(p, tk.idx, lane, get_x, tag, take);
@@ -1179,7 +1184,12 @@ int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   }
   // While the routing resolves only the router rows load: any request issued
   // behind a full memory queue waits microseconds, and every routing step is one.
-  p.sh_after = p.k - 1 < kSharedAfter ? p.k - 1 : kSharedAfter;
+  // Int4 (static tickets): S right after R.  A wave's second task is the one a grid's
+  // worth of tasks after its first, so the R and S waves, done before the routing
+  // resolves, take the gate/up tasks that do not fit in the first round and start them
+  // with the others (S after G1 left G7 to the G0 waves, after their first task:
+  // 26.7 -> 24.9 us at the full-size layer).
+  p.sh_after = p.q4 ? -1 : p.k - 1 < kSharedAfter ? p.k - 1 : kSharedAfter;
   p.sd_after = p.k - 1 < p.sh_after + kDownLag ? p.k - 1 : p.sh_after + kDownLag;
   p.n_tasks = p.n_r + p.n_s + p.n_sd + p.k * (p.n_g + p.n_d);
   int grid = resident_blocks(k);

@@ -2,7 +2,8 @@
 
 The model restates the scheduling of tarfa_amd/csrc/decode_fused.hip: the task list order of
 ``decode_task`` (router rows R, then per slot j the gate/up tasks Gj, the down tasks D(j - 8)
-after G j for j >= 8, the shared gate/up S after G(sh_after), the shared down SD after
+after G j for j >= 8, the shared gate/up S after G(sh_after) -- right after R when sh_after
+< 0, the int4 order --, the shared down SD after
 G(sd_after), the remaining D last), its dependencies (S: none; SD: every S; Gj: every R;
 Dj: every Gj; the last slot's D tasks, which combine, also every other slot's D task of the
 same rows and the SD task of those rows), 32 queues (task t in queue t % 32, served by wave
@@ -22,6 +23,8 @@ KDOWNLAG, QUEUES, WAVES = 8, 32, 4
 def task_list(n_r, n_s, n_sd, n_g, n_d, k, sh_after, sd_after):
     """[(type, slot, idx)] in the order of decode_task (decode_fused.hip)."""
     out = [("R", 0, i) for i in range(n_r)]
+    if sh_after < 0:
+        out += [("S", 0, i) for i in range(n_s)]
     for j in range(k):
         out += [("G", j, i) for i in range(n_g)]
         if j >= KDOWNLAG:
@@ -118,12 +121,28 @@ def simulate(tasks, deps, grid, dynamic, arrival, capacity, max_steps=5000):
 
 
 FULL = dict(n_r=65, n_s=512, n_sd=320, n_g=512, n_d=320, k=8, sh_after=1, sd_after=7)
+# Int4 mode at the same layer: 4 row pairs per gate/up task, 16 rows per down task, S first.
+FULL_INT4 = dict(n_r=65, n_s=256, n_sd=320, n_g=256, n_d=160, k=8, sh_after=-1, sd_after=7)
 
 
-def _graph():
-    tasks = task_list(**FULL)
-    deps = dependencies(tasks, FULL["k"])
+def _graph(shape=FULL):
+    tasks = task_list(**shape)
+    deps = dependencies(tasks, shape["k"])
     return tasks, deps
+
+
+def test_int4_order_completes_with_static_tickets():
+    tasks, deps = _graph(FULL_INT4)
+    assert len(tasks) == 65 + 256 + 320 + 8 * (256 + 160)
+    assert tasks[65] == ("S", 0, 0) and tasks[65 + 256] == ("G", 0, 0)
+    for i, d in enumerate(deps):
+        assert all(j < i for j in d), (i, tasks[i])
+    assert simulate(tasks, deps, 512, False, [0] * 512, capacity=512)[0]
+    # The second round (tasks 2048 + w for wave w's first task w): the R and S waves take the
+    # gate/up tasks left over from the first round, every other wave a down task or none.
+    second = tasks[2048:2048 + 65 + 256]
+    assert all(ty == "G" for ty, _, _ in second)
+    assert all(ty in ("SD", "D") for ty, _, _ in tasks[2048 + 65 + 256:])
 
 
 def test_every_dependency_points_to_a_smaller_task():
