@@ -1262,11 +1262,20 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
   for (int c = 0; c < MAXC; ++c)
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[c][q] = 0.f;
+  // a = bf16(a + bf16(x * wt)) per column; the roundings two columns per hardware
+  // conversion (round to nearest even, as the bit-operation form).
   auto add = [&](float* a, const u32x4 v, float wt) {
     const float x[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
                         bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
 #pragma unroll
-    for (int q = 0; q < 8; ++q) a[q] = rbf16(a[q] + rbf16(x[q] * wt));
+    for (int q = 0; q < 8; q += 2) {
+      float p0 = x[q] * wt, p1 = x[q + 1] * wt;
+      rbf16x2_hw(p0, p1);
+      float s0 = a[q] + p0, s1 = a[q + 1] + p1;
+      rbf16x2_hw(s0, s1);
+      a[q] = s0;
+      a[q + 1] = s1;
+    }
   };
   // The entries in rank order (wave-uniform), then per chunk every row's load issued before
   // the additions, which stay in rank order.
@@ -1300,10 +1309,10 @@ __global__ __launch_bounds__(256) void k_combine(const int32_t* ids32, const int
       for (int q = 0; q < 8; ++q) acc[c][q] = hx[q] + acc[c][q];
     }
     u32x4 o;
-    o.x = f32_to_bf16(acc[c][0]) | ((uint32_t)f32_to_bf16(acc[c][1]) << 16);
-    o.y = f32_to_bf16(acc[c][2]) | ((uint32_t)f32_to_bf16(acc[c][3]) << 16);
-    o.z = f32_to_bf16(acc[c][4]) | ((uint32_t)f32_to_bf16(acc[c][5]) << 16);
-    o.w = f32_to_bf16(acc[c][6]) | ((uint32_t)f32_to_bf16(acc[c][7]) << 16);
+    o.x = bf16x2_bits_hw(acc[c][0], acc[c][1]);
+    o.y = bf16x2_bits_hw(acc[c][2], acc[c][3]);
+    o.z = bf16x2_bits_hw(acc[c][4], acc[c][5]);
+    o.w = bf16x2_bits_hw(acc[c][6], acc[c][7]);
     *reinterpret_cast<u32x4*>(out + (size_t)t * H + col) = o;
   }
 }
