@@ -812,13 +812,14 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           char* rowp = stg + (ii * 16 + e) * TCB;
+          // Hardware conversions (round to nearest even), two values each.
           if constexpr (UP) {
-            *reinterpret_cast<uint16_t*>(rowp + cb[0]) =
-                f32_to_bf16(swiglu_bf16(rbf16(acc[i][0][e]), rbf16(acc[i][1][e])));
+            *reinterpret_cast<uint16_t*>(rowp + cb[0]) = swiglu_bits_hw(acc[i][0][e], acc[i][1][e]);
           } else {
-#pragma unroll
-            for (int nb = 0; nb < kPNB; ++nb)
-              *reinterpret_cast<uint16_t*>(rowp + cb[nb]) = f32_to_bf16(acc[i][nb][e]);
+            static_assert(kPNB == 2, "one conversion per row of the wave's two weight blocks");
+            const uint32_t w = bf16x2_bits_hw(acc[i][0][e], acc[i][1][e]);
+            *reinterpret_cast<uint16_t*>(rowp + cb[0]) = (uint16_t)w;
+            *reinterpret_cast<uint16_t*>(rowp + cb[1]) = (uint16_t)(w >> 16);
           }
         }
       }
