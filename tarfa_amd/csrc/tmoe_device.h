@@ -186,7 +186,14 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) { return rbf16(rb
 // fp32 g / (1 + e^-g)).  The prefill GEMM epilogue's form, where an IEEE division and
 // software rounding would hold up the weight stream.
 typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
-// Two fp32 values to bf16 bits in one hardware conversion (low half: a).
+__device__ __forceinline__ uint16_t swiglu_bits_hw(float gacc, float uacc) {
+  const uint32_t gu = __builtin_bit_cast(uint32_t, bf16x2_hw{(__bf16)gacc, (__bf16)uacc});
+  const float g = __uint_as_float(gu << 16), u = __uint_as_float(gu & 0xFFFF0000u);
+  const float s = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + expf(-g)));
+  return __builtin_bit_cast(uint16_t, (__bf16)(s * u));
+}
+// Two fp32 values to bf16 bits in one hardware conversion (v_cvt_pk_bf16_f32: round to nearest
+// even, as f32_to_bf16, for every value but NaN payloads; low half: a).
 __device__ __forceinline__ uint32_t bf16x2_bits_hw(float a, float b) {
   return __builtin_bit_cast(uint32_t, bf16x2_hw{(__bf16)a, (__bf16)b});
 }
@@ -195,12 +202,6 @@ __device__ __forceinline__ void rbf16x2_hw(float& a, float& b) {
   const uint32_t w = bf16x2_bits_hw(a, b);
   a = __uint_as_float(w << 16);
   b = __uint_as_float(w & 0xFFFF0000u);
-}
-__device__ __forceinline__ uint16_t swiglu_bits_hw(float gacc, float uacc) {
-  const uint32_t gu = __builtin_bit_cast(uint32_t, bf16x2_hw{(__bf16)gacc, (__bf16)uacc});
-  const float g = __uint_as_float(gu << 16), u = __uint_as_float(gu & 0xFFFF0000u);
-  const float s = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + expf(-g)));
-  return __builtin_bit_cast(uint16_t, (__bf16)(s * u));
 }
 
 }  // namespace tmoe
