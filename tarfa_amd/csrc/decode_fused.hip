@@ -84,6 +84,7 @@ constexpr int q4_down_rows(int MI) { return MI <= 2 ? 16 : 8; }
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
+constexpr int kSharedDelay = 64;       // exact-bf16: the shared gate/up tasks' start delay, x 64 cycles (~2 us)
 // Tickets: every one drawn from a per-queue counter (exact-bf16 mode) or static
 // (rank + users * i; int4 mode, where the draw's round trip is not hidden by the short
 // tasks' loads).
@@ -964,6 +965,15 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       if (p.trace) ts_route = __builtin_amdgcn_s_memrealtime();
       // The first gate/up task of slot 0 publishes (after R, and after S when S leads).
       if (t == p.n_r + (p.sh_after < 0 ? p.n_s : 0)) publish_routing(p, lane, rwc);
+    }
+    // Exact-bf16 mode: the shared gate/up tasks (all drawn at entry) issue their loads ~2 us
+    // late.  Issued at once, their 10.5 MB sits in the memory queues in front of the router
+    // rows loaded beside them, and the routing is the critical path; the shared expert has
+    // slack until the routing resolves (~8 us).  36.4 -> 35.3 us at the full-size layer.  Int4
+    // mode keeps them at once: its S waves take the last gate/up tasks next (25.2 -> 26.2 us
+    // with the delay).
+    if constexpr (DYN) {
+      if (tk.type == kTS && i == 0) __builtin_amdgcn_s_sleep(kSharedDelay);
     }
     if (tk.type == kTR) {
       task_router<MH, EXACT, LN>(p, tk.idx, lane, get_x, tag, take);
