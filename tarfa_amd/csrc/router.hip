@@ -2,10 +2,14 @@
 // one-wave-per-token softmax / top-k / renormalise.
 //   transformers/.../modeling_qwen3_5_moe.py:768-776 (Qwen3_5MoeTopKRouter.forward),
 //   with fp32 logits in place of the hidden-dtype F.linear at :770.
+#include <stdlib.h>
+
 #include "tmoe_gemv.h"
 #include "tmoe_ws.h"
 
 namespace tmoe {
+
+constexpr int kRouterMfmaFrom = 128;   // tokens from which the logits run as an MFMA GEMM (equal at 32..128)
 
 // logits[t, e] = sum_h x[t, h] * wg[e, h] in fp32.  Block (t, y) of a (T, Y) grid: wave w
 // handles experts 16 y + 4 w .. + 3, then 16 (y + Y) + 4 w, ... (4 rows in flight per
@@ -32,6 +36,87 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restric
   }
 }
 
+// The same logits for many tokens as a GEMM on the matrix cores: v_mfma_f32_16x16x32_bf16
+// (exact bf16 products, fp32 accumulation).  Block (tb, eb) of 4 waves computes tokens
+// 32 tb .. + 31 x experts 32 eb .. + 31 (four 16 x 16 blocks); the K steps (32 wide) are
+// dealt round-robin to the 4 waves (step s to wave s % 4), and the waves' partial sums are
+// added through LDS in wave order, so each logit is one fixed-order fp32 sum.  Operand
+// fragments come straight from memory, lane l holding row l % 16 and k = 8 (l / 16) .. + 7
+// of a step (16 bytes), for the token rows (A) and the router rows (B); rows past T or E
+// repeat the last one and are never stored.  The GEMV form above reads the whole router
+// weight once per token (1.3 GB of L2 reads per 1000 tokens at H = 2560, E = 256); this
+// reads it once per 32 tokens.  H a multiple of 32.
+typedef __bf16 rt_bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kRtUnroll = 8;   // k steps of a wave whose loads are issued together
+__global__ __launch_bounds__(256) void k_router_logits_mfma(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ wg, int T, int H, int E,
+                                                            float* __restrict__ logits) {
+  __shared__ f32x4 red[4][4][64];   // [wave][block (i, j)][lane]
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int t0 = (int)blockIdx.x * 32, e0 = (int)blockIdx.y * 32;
+  const int r = lane & 15, kq = (lane >> 4) * 8;
+  const uint16_t* pa[2];
+  const uint16_t* pb[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    pa[i] = x + (size_t)min(t0 + 16 * i + r, T - 1) * H + kq;
+    pb[i] = wg + (size_t)min(e0 + 16 * i + r, E - 1) * H + kq;
+  }
+  f32x4 c[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) c[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](const u32x4 (&a)[2], const u32x4 (&b)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        c[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rt_bf16x8, a[i]),
+                                                          __builtin_bit_cast(rt_bf16x8, b[j]), c[i][j], 0, 0, 0);
+  };
+  const int nsteps = H / 32;
+  int st = wid;
+  for (; st + 4 * (kRtUnroll - 1) < nsteps; st += 4 * kRtUnroll) {
+    u32x4 a[kRtUnroll][2], b[kRtUnroll][2];
+#pragma unroll
+    for (int u = 0; u < kRtUnroll; ++u)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[u][i] = ld16(pa[i] + 32 * (st + 4 * u));
+        b[u][i] = ld16(pb[i] + 32 * (st + 4 * u));
+      }
+#pragma unroll
+    for (int u = 0; u < kRtUnroll; ++u) step(a[u], b[u]);
+  }
+  for (; st < nsteps; st += 4) {
+    u32x4 a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      a[i] = ld16(pa[i] + 32 * st);
+      b[i] = ld16(pb[i] + 32 * st);
+    }
+    step(a, b);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) red[wid][2 * i + j][lane] = c[i][j];
+  __syncthreads();
+  // Wave w stores block (i, j) = (w / 2, w % 2): lane l holds tokens 16 i + 4 (l / 16) + q,
+  // expert 16 j + l % 16.
+  const int i = wid >> 1, j = wid & 1;
+  const f32x4 v = ((red[0][wid][lane] + red[1][wid][lane]) + red[2][wid][lane]) + red[3][wid][lane];
+  const int e = e0 + 16 * j + r;
+  if (e < E) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = t0 + 16 * i + 4 * (lane >> 4) + q;
+      if (t < T) logits[(size_t)t * E + e] = v[q];
+    }
+  }
+}
+
 // One wave per token.
 template <int MAXEPL>
 __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int T, int E, int k,
@@ -51,6 +136,15 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
 
 int launch_router_logits(const uint16_t* x, const uint16_t* wg, int T, int H, int E, float* logits,
                          hipStream_t s) {
+  static const int mfma_from = [] {
+    const char* e = getenv("TMOE_ROUTER_MFMA_FROM");
+    return e ? atoi(e) : kRouterMfmaFrom;
+  }();
+  if (T >= mfma_from && H % 32 == 0) {
+    const dim3 g((T + 31) / 32, (E + 31) / 32);
+    hipLaunchKernelGGL(k_router_logits_mfma, g, dim3(256), 0, s, x, wg, T, H, E, logits);
+    return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+  }
   const int nc = (H + 511) / 512;
   const dim3 g(T, T < 512 ? (E + 15) / 16 : 1);
   switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
