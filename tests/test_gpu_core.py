@@ -56,7 +56,7 @@ def _check_routing(ids, w, logits_ref, k, what):
 
 
 @pytest.mark.parametrize("H,E,k,T", [(1024, 32, 8, 64), (2560, 256, 8, 64), (512, 64, 4, 7), (2560, 256, 8, 1000),
-                                     (1024, 32, 8, 333), (2560, 256, 8, 40)])
+                                     (1024, 32, 8, 333), (2560, 256, 8, 40), (1024, 100, 6, 200)])
 def test_router_topk_multi_token(gpu, H, E, k, T):
     shape = MoEShape(H, E, 256, k)
     wg = seeded.make_layer(MoEShape(H, E, 8, k), seed=5, device=gpu).router_w
