@@ -212,7 +212,8 @@ __device__ __forceinline__ int logit_copy(const DecodeParams& p) { return (int)(
 // (valid) by the block's resolving wave (poller).
 struct RouteLds {
   uint32_t word[kRouteWords];
-  uint32_t valid;
+  uint32_t valid;    // the expert ids (words kRwId ..) are set
+  uint32_t wvalid;   // the weights and the shared gate (words kRwW ..) are set
   uint32_t poller;
 };
 constexpr uint32_t kUnseenWord = 0xFFFFFFFFu;
@@ -409,7 +410,6 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
   __builtin_amdgcn_s_setprio(3);   // the routing gates every expert task: issue ahead of streaming waves
   const uint64_t* lg = p.lg64 + (size_t)logit_copy(p) * p.lg_stride;
   float v[MAXEPL];
-  float gl = 0.f;
   if (p.logits_in) {
 #pragma unroll
     for (int i = 0; i < MAXEPL; ++i) {
@@ -420,24 +420,21 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
   const uint64_t ts_entry = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
   uint64_t ts_ok = 0;
   uint32_t rounds = 0;
-  if (!p.logits_in || has_sh) {
+  if (!p.logits_in) {
     // Every load of a poll round is issued before any is waited for: the
-    // addresses are clamped into the logit words, never skipped.
+    // addresses are clamped into the logit words, never skipped.  The shared-gate
+    // logit is not waited for here: only the combine needs it.
     Backoff<1> b;
     for (;;) {
       uint64_t w[MAXEPL];
 #pragma unroll
       for (int i = 0; i < MAXEPL; ++i) w[i] = ld64c(lg + min(lane + 64 * i, p.E - 1));
-      const uint64_t wg = ld64c(lg + p.E);
-      bool ok = !has_sh || has_tag(wg, tag);
-      gl = __uint_as_float((uint32_t)wg);
-      if (!p.logits_in) {
+      bool ok = true;
 #pragma unroll
-        for (int i = 0; i < MAXEPL; ++i) {
-          const bool in = lane + 64 * i < p.E;
-          ok &= !in || has_tag(w[i], tag);
-          v[i] = in ? __uint_as_float((uint32_t)w[i]) : -INFINITY;
-        }
+      for (int i = 0; i < MAXEPL; ++i) {
+        const bool in = lane + 64 * i < p.E;
+        ok &= !in || has_tag(w[i], tag);
+        v[i] = in ? __uint_as_float((uint32_t)w[i]) : -INFINITY;
       }
       ++rounds;
       if (__all(ok)) break;
@@ -497,6 +494,12 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
     }
   }
   const uint64_t ts_sel = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  // The ids go to the block at once: the expert tasks need them, the weights and the gate
+  // only their combine.
+  if (lane < kRwW) L.word[kRwId + lane] = (uint32_t)my_id;
+  __threadfence_block();
+  if (lane == 0) __hip_atomic_store(&L.valid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __builtin_amdgcn_s_setprio(0);
   // Softmax over all E in fp32 (max-subtracted), renormalised over the k
   // selected, rounded to bf16 -- one slot per lane.
   float ls = 0.f;
@@ -512,13 +515,22 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
   // Route words: lanes 0..7 the ids (E for slots past k), lanes 8..15 the weights of
   // slots 0..7, lane 16 the gate.
   const uint32_t wsrc = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane - kRwW) & 63) * 4, (int)wb);
+  // The shared-gate logit (row E of the router tasks), polled now that the ids are out.
+  float gl = 0.f;
+  if (has_sh) {
+    Backoff<4> b;
+    for (;;) {
+      const uint64_t wg = ld64c(lg + p.E);
+      gl = __uint_as_float((uint32_t)wg);
+      if (has_tag(wg, tag)) break;
+      if (!b.step(err)) break;
+    }
+  }
   const uint32_t gate = has_sh ? f32_to_bf16(sigmoid_f32(rbf16(gl))) : 0u;
-  const uint32_t word = lane < kRwW ? (uint32_t)my_id : lane < kRwGate ? wsrc : gate;
   const uint64_t ts_soft = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
-  if (lane < kRouteWords) L.word[lane] = word;
+  if (lane >= kRwW && lane < kRouteWords) L.word[lane] = lane < kRwGate ? wsrc : gate;
   __threadfence_block();
-  if (lane == 0) __hip_atomic_store(&L.valid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  __builtin_amdgcn_s_setprio(0);
+  if (lane == 0) __hip_atomic_store(&L.wvalid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   if (p.trace && lane == 0) {
     uint64_t* rec = p.trace + kTraceHeader + (size_t)p.n_tasks * kTraceTaskWords + 2 * (size_t)gridDim.x * 4 +
                     8 * (size_t)blockIdx.x;
@@ -550,7 +562,17 @@ __device__ __forceinline__ void route_fetch(const DecodeParams& p, int lane, uin
     if (!b.step(err)) break;
   }
   __threadfence_block();
-  if (lane < kRouteWords) rwc = L.word[lane];
+  if (lane < kRwW) rwc = L.word[kRwId + lane];
+}
+
+// The routing weights and the shared gate into the wave's cache (lanes kRwW ..): set by the
+// block's resolving wave right after the ids, long before any combine asks for them.
+__device__ __forceinline__ void route_weights(int lane, uint32_t& rwc, uint32_t* err, RouteLds& L) {
+  Backoff<16> b;
+  while (!__hip_atomic_load(&L.wvalid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+    if (!b.step(err)) break;
+  __threadfence_block();
+  if (lane >= kRwW && lane < kRouteWords) rwc = L.word[lane];
 }
 
 // The call's routing outputs (ids, bf16 weights, heat counts, logits), written once: by
@@ -877,12 +899,14 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   __shared__ RouteLds s_rt;     // the block's view of the routing
   if (threadIdx.x == 0) {
     s_rt.valid = 0u;
+    s_rt.wvalid = 0u;
     s_rt.poller = 0u;
   }
   __syncthreads();
 
   uint32_t rwc = kUnseenWord;   // this wave's routing cache (lane layout of RouteWord)
   bool routed = p.ids_in != nullptr;
+  bool weighted = p.ids_in != nullptr;   // rwc holds the weights and the gate too
   if (p.ids_in) {
     // Caller-supplied routing (ids outside [0, E) are skipped; E is the sentinel).
     if (lane0 < p.k) {
@@ -963,8 +987,15 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       route_fetch(p, lane, rwc, tag, err, s_rt);
       routed = true;
       if (p.trace) ts_route = __builtin_amdgcn_s_memrealtime();
-      // The first gate/up task of slot 0 publishes (after R, and after S when S leads).
-      if (t == p.n_r + (p.sh_after < 0 ? p.n_s : 0)) publish_routing(p, lane, rwc);
+    }
+    if (tk.type == kTD && tk.slot == p.k - 1) {
+      // The combining tasks need the weights and the gate; the first of them publishes the
+      // call's routing outputs.
+      if (!weighted) {
+        route_weights(lane, rwc, err, s_rt);
+        weighted = true;
+      }
+      if (tk.idx == 0) publish_routing(p, lane, rwc);
     }
     // Exact-bf16 mode: the shared gate/up tasks (all drawn at entry) issue their loads ~2 us
     // late.  Issued at once, their 10.5 MB sits in the memory queues in front of the router
