@@ -41,21 +41,22 @@
 //     weight rows (queued kDownLag slots after its gate/up tasks, the activations
 //     are normally complete); stale words are re-polled with coherent loads.
 //   - Each wave caches the routing; the block's copy in LDS is resolved once.
-//   - Queue q (of 32) is served by wave q % 4 of the blocks b with b % 8 == q / 4
-//     (one XCD) and holds tasks q, q + 32, ...  In exact-bf16 mode every ticket, a
-//     wave's first included, is drawn from the queue's counter: the first at entry
+//   - Exact-bf16 mode: queue q (of 128) is served by wave q % 4 of the blocks b with
+//     group(b) == q / 4, group(b) = (b % 8) * 4 + (b / 8) % 4 (the blocks of one XCD fall in 4
+//     groups), and holds tasks q, q + 128, ...  (128 counters: 16 waves per counter line
+//     instead of 64 keep the draws that the routing releases all at once from serialising on
+//     32 lines.)  Int4 mode uses 32 queues, one group per XCD (group(b) = b % 8).  Every
+//     ticket, a wave's first included, is drawn from the queue's counter: the first at entry
 //     (its round trip overlaps the epoch load), every later one when a task starts,
 //     read after the task's loads and before its stores (gfx9 counts stores in
 //     vmcnt, and vector memory returns in issue order).  A queue's tasks are so
 //     claimed in list order and only by running waves, and a task waits only on
 //     tasks with smaller indices: the smallest unfinished task is always some running
 //     wave's current task and can finish, whatever subset of the grid is resident,
-//     as long as every queue has one running wave (one block of the grid on each XCD;
-//     tests/test_ticket_progress.py simulates the task graph).  In int4 mode the
-//     tickets are static, r + users i for the wave of rank r = b / 8 (a dynamic draw
-//     per task costs the short int4 tasks 26.7 -> 31.3 us), which relies on the whole
-//     grid being resident: the launch sizes it from the occupancy (kBlocksPerCU), and
-//     a wait that still starves (another kernel holding CUs) ends in kErrTimeout.
+//     as long as every queue has one running wave (one block of each of the 32 groups;
+//     tests/test_ticket_progress.py simulates the task graph).  Int4 mode draws its tickets
+//     the same way (its short tasks hide less of the draw's round trip, but static tickets
+//     would need the whole grid resident).
 //   - Every poll backs off and is bounded (kErrTimeout on expiry).
 //   - The last wave to leave a queue re-zeroes its exit count; the last queue to
 //     drain advances the epoch.
@@ -85,14 +86,25 @@ constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (lar
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
 constexpr int kSharedDelay = 64;       // exact-bf16: the shared gate/up tasks' start delay, x 64 cycles (~2 us)
-// Tickets: every one drawn from a per-queue counter (exact-bf16 mode) or static
-// (rank + users * i; int4 mode, where the draw's round trip is not hidden by the short
-// tasks' loads).
+// Tickets: every one drawn from a per-queue counter, in both modes, so the call completes
+// whatever subset of the grid is resident (the int4 mode's short tasks hide less of the draw's
+// round trip than the exact-bf16 ones, but static tickets would need the whole grid resident).
 template <bool Q4>
-constexpr bool dynamic_tickets() { return !Q4; }
+constexpr bool dynamic_tickets() { return true; }
 constexpr int kBlocksPerCU = 2;        // resident blocks per CU (bounds the bytes in flight per XCD)
 constexpr uint32_t kSpinLimit = 1u << 20;   // polls, each >= 64 cycles apart: never reached by a healthy graph
-static_assert(kQueues == 8 * kWaves, "queue q is served by wave q % 4 of the blocks b with b % 8 == q / 4");
+static_assert(kQueues == 32 * kWaves, "queue q is served by wave q % 4 of the blocks of group q / 4 (32 groups)");
+// Queue groups of a mode: exact-bf16 32 (each XCD's blocks in 4 interleaved groups, 16 waves
+// per counter line), int4 8 (one per XCD; 64 waves per line: measured 30.3 us per layer against
+// 33.3 with 32 groups, its few short tasks per wave gaining more from the longer queues).
+template <bool Q4>
+constexpr int queue_groups() { return Q4 ? 8 : 32; }
+// The block group of block b (NG groups): its XCD (b % 8), and with NG = 32 one of 4
+// interleaved groups on it.
+template <int NG>
+__device__ __forceinline__ int block_group(uint32_t b) {
+  return NG == 8 ? (int)(b % 8u) : (int)(b % 8u) * 4 + (int)((b / 8u) % 4u);
+}
 
 enum TaskType { kTR = 0, kTS = 2, kTSD = 3, kTG = 4, kTD = 5 };
 
@@ -842,7 +854,7 @@ __device__ __forceinline__ void finish_call(const DecodeParams& p, uint32_t tag,
     for (size_t i = lane; i < p.handoff_words; i += 64) st64c(w + i, 0ull);
   }
   const uint32_t epoch = wrap ? 0u : tag;
-  if (lane < kQueues) st32c(line(p, kLnQueue + lane) + kQueueEpochWord, epoch);
+  for (int j = lane; j < kQueues; j += 64) st32c(line(p, kLnQueue + j) + kQueueEpochWord, epoch);
   if (lane == 0) {
     st32c(line(p, kLnQueuesDone), 0u);
     st32c(line(p, kLnEpoch), epoch);
@@ -879,10 +891,15 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     for (int o = 0; o < (int)(sizeof(DecodeParams) / 4); o += 16) touch ^= ka[o];
     if (touch == 0x9E3779B9u && threadIdx.x == 0x3FF) err = nullptr;   // never taken: only makes the loads needed
   }
-  const int q = (int)(blockIdx.x % 8) * kWaves + wid;
+  constexpr int NG = queue_groups<Q4>();
+  constexpr int NQ = NG * kWaves;            // queues of this mode (the first NQ of kQueues)
+  const int grp = block_group<NG>(blockIdx.x);
+  const int q = grp * kWaves + wid;
   uint32_t* queue = line(p, kLnQueue + q);
-  const uint32_t users = (gridDim.x - (uint32_t)(q / kWaves) + 7u) / 8u;
-  const uint32_t rank = blockIdx.x / 8u;
+  // Blocks of this group: b = g0 + NG r, r = 0, 1, ... (g0 = x + 8 g for group 4 x + g of 32).
+  const uint32_t g0 = NG == 8 ? (uint32_t)grp : (uint32_t)(grp / 4 + 8 * (grp % 4));
+  const uint32_t users = (gridDim.x - g0 + NG - 1u) / (uint32_t)NG;
+  const uint32_t rank = blockIdx.x / (uint32_t)NG;
   constexpr bool DYN = dynamic_tickets<Q4>();
   uint32_t* draw = line(p, kLnQueueExit + q) + kQueueDrawWord;
   // Exact-bf16 mode: the first ticket, drawn at once; read where the first task starts.
@@ -936,7 +953,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   // the routing, which this overlaps (router waves form it inside their task instead,
   // behind their rows' loads).
   if constexpr (LN) {
-    if (q + kQueues * (int)rank >= p.n_r) {
+    if (q + NQ * (int)rank >= p.n_r) {
       load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane0);
       have_x = true;
     }
@@ -951,7 +968,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     for (int i = 0; i < kTraceHeader; ++i) p.trace[i] = hdr[i];
   }
   for (uint32_t i = 0;; ++i) {
-    const int t = q + kQueues * (int)ticket;
+    const int t = q + NQ * (int)ticket;
     if (t >= p.n_tasks) break;
     uint64_t ts_start = 0, ts_route = 0, ts_take = 0;
     if (p.trace) ts_start = __builtin_amdgcn_s_memrealtime();
@@ -1003,7 +1020,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     // slack until the routing resolves (~8 us).  36.4 -> 35.3 us at the full-size layer.  Int4
     // mode keeps them at once: its S waves take the last gate/up tasks next (25.2 -> 26.2 us
     // with the delay).
-    if constexpr (DYN) {
+    if constexpr (!Q4) {
       if (tk.type == kTS && i == 0) __builtin_amdgcn_s_sleep(kSharedDelay);
     }
     if (tk.type == kTR) {
@@ -1092,7 +1109,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
     if (add32c(line(p, kLnQueueExit + q), 1u) == users - 1u) {
       st32c(line(p, kLnQueueExit + q), 0u);
       st32c(draw, 0u);
-      fin = add32c(line(p, kLnQueuesDone), 1u) == (uint32_t)kQueues - 1u;
+      fin = add32c(line(p, kLnQueuesDone), 1u) == (uint32_t)NQ - 1u;
     }
   }
   if (__builtin_amdgcn_readfirstlane(fin)) finish_call(p, tag, lane0);
@@ -1237,7 +1254,7 @@ int decode_fused_launch(DecodeParams& p, bool run_router, hipStream_t s) {
   if (grid <= 0) return TMOE_ERR_HIP;
   const int need = (p.n_tasks + kWaves - 1) / kWaves;
   if (grid > need) grid = need;
-  if (grid < 8) grid = 8;   // every queue needs a wave
+  if (grid < 32) grid = 32;   // every queue needs a wave: one block of each group
   {
     std::lock_guard<std::mutex> lock(g_trace_mu);
     p.trace = g_trace && trace_words(p.n_tasks, grid * kWaves) * 8 <= g_trace_bytes ? g_trace : nullptr;

@@ -28,7 +28,7 @@ constexpr int kLine = 64;                 // uint32 per line
 // combine tiles of 64 output columns.
 constexpr int kSbMaxTokens = 16, kSbMaxEntries = 256, kSbTiles = 4096 / 64;
 constexpr int kLogitReplicas = 32;        // router logits published to this many copies (blocks poll one each)
-constexpr int kQueues = 32;               // task queues: 4 waves x 8 XCD-sized groups of blocks
+constexpr int kQueues = 128;              // task queues: 4 waves x 32 block groups (4 per XCD)
 enum SyncLine {
   kLnEpoch = 0,                           // word 0: epoch of the next call (tag = epoch + 1)
   kLnQueuesDone = 1,                      // queues fully drained this call

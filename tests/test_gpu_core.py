@@ -126,11 +126,12 @@ def test_decode_sentinel_and_invalid_ids(gpu):
         ws.status()
 
 
-# Fused-decode workspace layout: a status block (64 uint32), then 256-byte lines;
-# line 0 word 0 holds the epoch, lines 2..33 are the task queues, each with a copy
-# of the epoch in word 16 (read by that queue's waves).
+# Fused-decode workspace layout (tarfa_amd/csrc/tmoe_ws.h): a status block (64 uint32), then
+# 256-byte lines; line 0 word 0 holds the epoch, lines 2..129 are the 128 task queues, each
+# with a copy of the epoch in word 16 (read by that queue's waves).
+QUEUES = 128
 EPOCH_BYTE = 256
-EPOCH_COPIES = [256 + (2 + q) * 256 + 16 * 4 for q in range(32)]
+EPOCH_COPIES = [256 + (2 + q) * 256 + 16 * 4 for q in range(QUEUES)]
 
 
 def _epoch(ws):

@@ -6,9 +6,12 @@ after G j for j >= 8, the shared gate/up S after G(sh_after) -- right after R wh
 < 0, the int4 order --, the shared down SD after
 G(sd_after), the remaining D last), its dependencies (S: none; SD: every S; Gj: every R;
 Dj: every Gj; the last slot's D tasks, which combine, also every other slot's D task of the
-same rows and the SD task of those rows), 32 queues (task t in queue t % 32, served by wave
-q % 4 of the blocks b with b % 8 == q / 4), and the two ticket rules: every ticket drawn from
-the queue's counter (exact-bf16 mode) or static tickets rank + users i (int4 mode).
+same rows and the SD task of those rows), its queues (exact-bf16 mode: 128, task t in queue
+t % 128, served by wave q % 4 of the blocks b of group q / 4, group(b) = (b % 8) * 4 + (b / 8) % 4;
+int4 mode: 32, one group per XCD, group(b) = b % 8), and two
+ticket rules: every ticket drawn from the queue's counter (what both modes of the kernel do),
+or static tickets rank + users i (rank = b / 32), which the model keeps to show why they are
+not used.
 
 A step: every resident wave with no task draws its next ticket (or leaves when the ticket is
 past its queue's tasks); a wave whose task's dependencies are all done finishes it.  Blocks
@@ -17,7 +20,11 @@ has room (``capacity`` blocks), and leaves once its four waves have left.
 """
 import pytest
 
-KDOWNLAG, QUEUES, WAVES = 8, 32, 4
+KDOWNLAG, WAVES, GROUPS, GROUPS_INT4 = 8, 4, 32, 8
+
+
+def group(b, groups=GROUPS):
+    return b % 8 if groups == 8 else (b % 8) * 4 + (b // 8) % 4
 
 
 def task_list(n_r, n_s, n_sd, n_g, n_d, k, sh_after, sd_after):
@@ -63,13 +70,15 @@ def dependencies(tasks, k):
     return deps
 
 
-def simulate(tasks, deps, grid, dynamic, arrival, capacity, max_steps=5000):
+def simulate(tasks, deps, grid, dynamic, arrival, capacity, max_steps=5000, groups=GROUPS):
     """Run the model; returns (finished all, steps).  arrival[b] = step from which block b
     may become resident (None: never)."""
     n = len(tasks)
     done = [False] * n
-    counters = [0] * QUEUES
-    users = [(grid - qq // WAVES + 7) // 8 for qq in range(QUEUES)]
+    queues = groups * WAVES
+    counters = [0] * queues
+    first_block = {group(b, groups): b for b in reversed(range(groups))}
+    users = [(grid - first_block[qq // WAVES] + groups - 1) // groups for qq in range(queues)]
     waves = {}          # (block, wave) -> {"ticket_i": i, "task": t or None, "left": bool}
     resident, finished_blocks = set(), set()
     for step in range(max_steps):
@@ -86,15 +95,15 @@ def simulate(tasks, deps, grid, dynamic, arrival, capacity, max_steps=5000):
         for (b, w), st in waves.items():
             if b not in resident or st["left"]:
                 continue
-            q = (b % 8) * WAVES + w
+            q = group(b, groups) * WAVES + w
             if st["task"] is None:
                 if dynamic:
                     ticket = counters[q]
                     counters[q] += 1
                 else:
-                    ticket = b // 8 + users[q] * st["i"]
+                    ticket = b // groups + users[q] * st["i"]
                 st["i"] += 1
-                t = q + QUEUES * ticket
+                t = q + queues * ticket
                 if t >= n:
                     st["left"] = True
                     progressed = True
@@ -131,18 +140,22 @@ def _graph(shape=FULL):
     return tasks, deps
 
 
-def test_int4_order_completes_with_static_tickets():
+def test_int4_order_completes_with_drawn_tickets_and_partial_residency():
     tasks, deps = _graph(FULL_INT4)
     assert len(tasks) == 65 + 256 + 320 + 8 * (256 + 160)
     assert tasks[65] == ("S", 0, 0) and tasks[65 + 256] == ("G", 0, 0)
     for i, d in enumerate(deps):
         assert all(j < i for j in d), (i, tasks[i])
-    assert simulate(tasks, deps, 512, False, [0] * 512, capacity=512)[0]
-    # The second round (tasks 2048 + w for wave w's first task w): the R and S waves take the
-    # gate/up tasks left over from the first round, every other wave a down task or none.
-    second = tasks[2048:2048 + 65 + 256]
-    assert all(ty == "G" for ty, _, _ in second)
-    assert all(ty in ("SD", "D") for ty, _, _ in tasks[2048 + 65 + 256:])
+    g = GROUPS_INT4
+    assert simulate(tasks, deps, 512, True, [0] * 512, capacity=512, groups=g)[0]
+    # One block per XCD (blocks 0..7), room for 40 blocks, late blocks.
+    assert simulate(tasks, deps, 512, True, [0 if b < g else None for b in range(512)], capacity=512, groups=g)[0]
+    assert simulate(tasks, deps, 512, True, [0] * 512, capacity=40, groups=g)[0]
+    arrival = [0 if b % 7 == 0 or b < g else 3 + (b * 37) % 50 for b in range(512)]
+    assert simulate(tasks, deps, 512, True, arrival, capacity=96, groups=g)[0]
+    # Static tickets would not: one block never resident stalls the int4 order too.
+    arrival = [None if b == 9 else 0 for b in range(512)]
+    assert not simulate(tasks, deps, 512, False, arrival, capacity=512, groups=g)[0]
 
 
 def test_every_dependency_points_to_a_smaller_task():
@@ -161,19 +174,19 @@ def test_whole_grid_resident_completes(dynamic):
 
 def test_dynamic_tickets_complete_with_blocks_missing_or_late():
     tasks, deps = _graph()
-    # Only one block per XCD ever resident (blocks 0..7): every queue keeps one server.
-    arrival = [0 if b < 8 else None for b in range(512)]
+    # Only one block per group ever resident (blocks 0..31): every queue keeps one server.
+    arrival = [0 if b < GROUPS else None for b in range(512)]
     assert simulate(tasks, deps, 512, True, arrival, capacity=512)[0]
     # Room for 40 blocks: the rest arrive as earlier blocks leave.
     assert simulate(tasks, deps, 512, True, [0] * 512, capacity=40)[0]
     # Late blocks of every XCD, in a scrambled order.
-    arrival = [0 if b % 7 == 0 or b < 8 else 3 + (b * 37) % 50 for b in range(512)]
+    arrival = [0 if b % 7 == 0 or b < GROUPS else 3 + (b * 37) % 50 for b in range(512)]
     assert simulate(tasks, deps, 512, True, arrival, capacity=96)[0]
 
 
 def test_static_tickets_stall_when_a_block_is_missing():
     tasks, deps = _graph()
-    # Block 9 (rank 1 on XCD 1) never resident: its static first tickets (router tasks among
+    # Block 9 (group 5, rank 0) never resident: its static first tickets (router tasks among
     # them) are never run, and every gate/up task waits on the routing.
     arrival = [None if b == 9 else 0 for b in range(512)]
     assert not simulate(tasks, deps, 512, False, arrival, capacity=512)[0]
@@ -185,6 +198,6 @@ def test_static_tickets_stall_when_a_block_is_missing():
 
 def test_dynamic_tickets_need_one_server_per_queue():
     tasks, deps = _graph()
-    # No block ever on XCD 3: queues 12..15 have no server, and their tasks never run.
+    # No block ever on XCD 3: queues 48..63 have no server, and their tasks never run.
     arrival = [None if b % 8 == 3 else 0 for b in range(512)]
     assert not simulate(tasks, deps, 512, True, arrival, capacity=512)[0]
