@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 1
+#define TMOE_ABI_VERSION 2
 
 enum tmoe_status {
   TMOE_OK = 0,
@@ -87,6 +87,16 @@ int tmoe_fill_f32(float* dst, uint64_t n, uint64_t key, double scale, uint64_t s
 int tmoe_router_topk(const void* x, const void* router_w, const float* logits_in, int T, int H,
                      int E, int k, int64_t* ids_out, void* weights_out, float* logits_out,
                      uint32_t* heat, void* stream);
+
+/* The boundary's re-truncation of a routing that carries more experts than the engine runs
+ * (tarfa/engine/fused_int4.py:157-160, JTOPK at :17): per token keep the j largest of its k
+ * bf16 weights (equal weights keep the lower slot first), gather their ids, and renormalise
+ * in bf16: w'_r = bf16(w_r / bf16(sum of the kept weights)), the sum in fp32 in the kept
+ * (descending) order.  ids [T,k] int64, weights [T,k] bf16 -> ids_out [T,j], weights_out [T,j];
+ * 1 <= j <= k <= 16.
+ */
+int tmoe_topk_renorm_bf16(const int64_t* ids, const void* weights, int T, int k, int j,
+                          int64_t* ids_out, void* weights_out, void* stream);
 
 /* ---------------------------------------------------------------- dispatch (a3)
  * Token -> expert permutation of the reference's prefill

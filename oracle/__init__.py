@@ -30,6 +30,9 @@ Pinning status (each function is checked in ``tests/test_oracle.py`` and
 * bf16 rounding       pinned: torch ``Tensor.to(bfloat16)`` on 2^24 patterns + edge cases.
 * rng                 pinned: moments, determinism, device bit-equality (GPU test).
 * router_topk         pinned: torch CPU softmax/topk/renorm on untied inputs.
+* jtopk_truncate      pinned: torch CPU run of fused_int4.py:157-160 (topk, gather, bf16
+                      sum and division) on untied inputs; ties by brute force (the kept set
+                      and order under the lower-slot rule).
 * dispatch            pinned: brute force ``one_hot(...).permute(2,1,0)`` + ``torch.where``.
 * decode / prefill    pinned: torch CPU bf16 op chain written as the reference writes it
                       (``fused_int4.py:192-194`` / ``:239-244``) and transformers'

@@ -79,6 +79,28 @@ def router_topk(logits, k):
     return ids, w, probs
 
 
+def jtopk_truncate(ids, w, j):
+    """The reference's re-truncation at its experts boundary, tarfa/engine/fused_int4.py:157-160:
+    when a token carries more than j experts, ``tv, ti = w.topk(j)``, ``ids = gather(ids, ti)``,
+    ``w = tv / tv.sum(-1, keepdim=True)`` in the weights' dtype (bf16).  Selection by weight,
+    descending, equal weights keeping the lower slot first (torch's tie order is
+    implementation-defined); the sum of the kept bf16 values in fp32, in the kept order, rounded
+    to bf16; each quotient in fp32, rounded to bf16.  ids [T,k] int64, w [T,k] bf16 values ->
+    (ids [T,j], w [T,j]); k <= j returns the inputs."""
+    ids = np.atleast_2d(np.asarray(ids, np.int64))
+    w = np.atleast_2d(np.asarray(w, np.float32))
+    T, k = w.shape
+    if k <= j:
+        return ids, w
+    order = np.lexsort((np.broadcast_to(np.arange(k), (T, k)), -w.astype(np.float64)), axis=-1)[:, :j]
+    tv = np.take_along_axis(w, order, axis=-1)
+    s = np.zeros(T, np.float32)
+    for r in range(j):
+        s = (s + tv[:, r]).astype(np.float32)
+    out = rb((tv / rb(s)[:, None]).astype(np.float32))
+    return np.take_along_axis(ids, order, axis=-1), out
+
+
 def topk_gaps(logits, k):
     """Smallest gap between consecutive sorted logits among the top k+1 (per token)."""
     lg = np.sort(np.atleast_2d(np.asarray(logits, np.float64)), axis=-1)[:, ::-1]

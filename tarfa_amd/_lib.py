@@ -10,7 +10,7 @@ import re
 
 import torch  # noqa: F401  (must precede the library load, see module docstring)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtmoe.so")
 
 _c = ctypes
@@ -25,6 +25,7 @@ SIGNATURES = {
     "tmoe_fill_bf16": (_i, [_vp, _u64, _u64, _f, _u64, _vp]),
     "tmoe_fill_f32": (_i, [_vp, _u64, _u64, _d, _u64, _vp]),
     "tmoe_router_topk": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "tmoe_topk_renorm_bf16": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "tmoe_dispatch": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tmoe_experts_forward_bf16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "tmoe_moe_block_bf16": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
@@ -74,13 +75,18 @@ def lib():
     runtimes = _hip_runtimes_mapped()
     if len(runtimes) > 1:
         raise RuntimeError(f"two HIP runtimes mapped in one process: {sorted(runtimes)}")
+    # The version first: a library built from older sources may lack entry points named below.
+    ver = getattr(handle, "tmoe_abi_version", None)
+    if ver is None:
+        raise RuntimeError(f"{LIB_PATH} exports no tmoe_abi_version: rebuild with `python -m tarfa_amd.build`")
+    ver.restype, ver.argtypes = _i, []
+    v = ver()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"libtmoe ABI {v}, expected {ABI_VERSION}: rebuild with `python -m tarfa_amd.build`")
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype, fn.argtypes = res, args
     handle = _Bound(handle)
-    v = handle.tmoe_abi_version()
-    if v != ABI_VERSION:
-        raise RuntimeError(f"libtmoe ABI {v}, expected {ABI_VERSION}: rebuild with `python -m tarfa_amd.build`")
     _LIB = handle
     return handle
 

@@ -167,6 +167,43 @@ int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64,
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
 
+// The reference's re-truncation at its experts boundary (tarfa/engine/fused_int4.py:157-160):
+// when a token carries more than j routed experts, keep the j largest bf16 weights (equal
+// weights keep the lower slot first), gather their ids and renormalise in bf16:
+// w'_r = bf16(w_r / bf16(sum of the kept weights)), the sum in fp32 in the kept (descending)
+// order.  One thread per token; k <= 16.
+__global__ __launch_bounds__(256) void k_topk_renorm(const int64_t* __restrict__ ids,
+                                                     const uint16_t* __restrict__ w, int T, int k, int j,
+                                                     int64_t* __restrict__ ids_out, uint16_t* __restrict__ w_out) {
+  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (t >= T) return;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = i < k ? bf16_to_f32(w[(size_t)t * k + i]) : -INFINITY;
+  uint32_t used = 0;
+  int sel[16];
+  float sum = 0.f;
+  for (int r = 0; r < j; ++r) {
+    int best = -1;
+    float bv = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const bool cand = i < k && !((used >> i) & 1u) && (best < 0 || v[i] > bv);
+      best = cand ? i : best;
+      bv = cand ? v[i] : bv;
+    }
+    used |= 1u << best;
+    sel[r] = best;
+    sum += bv;
+  }
+  const float sb = rbf16(sum);
+  for (int r = 0; r < j; ++r) {
+    const int i = sel[r];
+    ids_out[(size_t)t * j + r] = ids[(size_t)t * k + i];
+    w_out[(size_t)t * j + r] = f32_to_bf16(bf16_to_f32(w[(size_t)t * k + i]) / sb);
+  }
+}
+
 int check_router_shape(int T, int H, int E, int k) {
   if (T < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E) return TMOE_ERR_SHAPE;
   if (H < 8 || H > 4096 || H % 8) return TMOE_ERR_SHAPE;
@@ -195,4 +232,14 @@ extern "C" int tmoe_router_topk(const void* x, const void* router_w, const float
       return TMOE_ERR_HIP;
   }
   return launch_router_topk(lg, T, E, k, ids_out, (uint16_t*)weights_out, nullptr, nullptr, heat, s);
+}
+
+extern "C" int tmoe_topk_renorm_bf16(const int64_t* ids, const void* weights, int T, int k, int j, int64_t* ids_out,
+                                     void* weights_out, void* stream) {
+  using namespace tmoe;
+  if (T < 1 || k < 1 || k > 16 || j < 1 || j > k) return TMOE_ERR_SHAPE;
+  if (!ids || !weights || !ids_out || !weights_out) return TMOE_ERR_NULL;
+  hipLaunchKernelGGL(k_topk_renorm, dim3((T + 255) / 256), dim3(256), 0, (hipStream_t)stream, ids,
+                     (const uint16_t*)weights, T, k, j, ids_out, (uint16_t*)weights_out);
+  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }

@@ -17,15 +17,18 @@ Around each call the boundary keeps what the reference's closure keeps
 (``telemetry()``; seconds come from HIP events, not from a forced synchronisation),
 and for decode calls the route-reuse counters (``routing_telemetry()``, recorded on
 the device).  Device-detected errors (an expert id outside [0, E], an expired
-bounded wait) are polled without stalling the compute stream: every
-``status_poll`` calls the workspace status word is copied to pinned host memory on a
-side stream, and the next call that finds the copy landed raises ``RuntimeError`` if it
-is set.  ``check_status()`` is the definitive check for the engine's own
-synchronisation points.
+bounded wait) are polled without stalling the compute stream: after every call (every
+``status_poll`` calls, default 1) the workspace status word is copied to pinned host
+memory on a side stream, and the next call that finds the copy landed raises
+``RuntimeError`` if it is set -- at the latest the first call after the engine's next
+synchronisation point (the reference synchronises after every call,
+tarfa/engine/fused_int4.py:203-204).  ``check_status()`` is the synchronous check.
 
 ``TmoeSparseMoeBlock`` mirrors ``Qwen3_5MoeSparseMoeBlock.forward``
 (transformers/.../modeling_qwen3_5_moe.py:787-798) with fp32 router logits.
 """
+import dataclasses
+import os
 import threading
 import types
 import weakref
@@ -34,7 +37,8 @@ import torch
 
 from ._lib import check
 from .int4_files import Int4LayerFile
-from .moe import MoEShape, Workspace, expert_table, expert_table_q4, expert_table_q4_rows, experts_forward, moe_block
+from .moe import (MoEShape, Workspace, expert_table, expert_table_q4, expert_table_q4_rows, experts_forward, moe_block,
+                  topk_renorm)
 from .residency import RouteTelemetry
 
 ENGINE_DTYPE = torch.bfloat16
@@ -47,7 +51,7 @@ class _CallBook:
     """Counters, event timing, route telemetry and the asynchronous status poll of one layer's calls."""
 
     def __init__(self, shape: MoEShape, workspace: Workspace, device, route_telemetry=True, timing=True,
-                 status_poll=64):
+                 status_poll=1):
         self.shape, self.workspace, self.device = shape, workspace, torch.device(device)
         self.counts = {k: 0 for k in _KINDS}
         self.seconds = {k: 0.0 for k in _KINDS}
@@ -213,8 +217,19 @@ class ExpertStore:
         self.book.check_status()
 
 
-def make_experts_forward(store: ExpertStore):
-    """The forward(self, hidden_states, top_k_index, top_k_weights) to bind on an experts module."""
+def engine_jtopk():
+    """The reference engine's JTOPK: experts run per token (environment, default 8;
+    tarfa/engine/fused_int4.py:17)."""
+    return int(os.environ.get("JTOPK", "8"))
+
+
+def make_experts_forward(store: ExpertStore, jtopk=None):
+    """The forward(self, hidden_states, top_k_index, top_k_weights) to bind on an experts module.
+    A routing with more than ``jtopk`` experts per token (default: engine_jtopk()) is first cut
+    to its jtopk largest weights and renormalised, as the reference does (fused_int4.py:157-160)."""
+    jtopk = engine_jtopk() if jtopk is None else int(jtopk)
+    if jtopk < 1:
+        raise ValueError(f"JTOPK must be at least 1, got {jtopk}")
 
     def forward(self, hidden_states, top_k_index, top_k_weights):
         # Returns a new tensor and mutates no input (fused_int4.py:161).  T == 1 accumulates
@@ -225,9 +240,14 @@ def make_experts_forward(store: ExpertStore):
         x = hidden_states.contiguous()
         ids = top_k_index.contiguous()
         w = top_k_weights.to(ENGINE_DTYPE).contiguous()
+        shape = store.shape
+        if w.shape[-1] > jtopk:
+            ids, w = topk_renorm(ids, w, jtopk)
+        if ids.shape[-1] != shape.top_k:
+            shape = dataclasses.replace(shape, top_k=ids.shape[-1])
         decode = x.shape[0] == 1
         return store.book.call("decode" if decode else "prefill",
-                               lambda: experts_forward(store.shape, x, ids, w, store.table, store.workspace),
+                               lambda: experts_forward(shape, x, ids, w, store.table, store.workspace),
                                record_ids=ids if decode else None)
 
     return forward
@@ -246,13 +266,14 @@ def _check_dtype(module, what):
                             "engine must be built with dtype=torch.bfloat16")
 
 
-def install_experts(experts, store: ExpertStore):
-    """Bind the libtmoe routed-compute step on an experts module instance (fused_int4.py:262)."""
+def install_experts(experts, store: ExpertStore, jtopk=None):
+    """Bind the libtmoe routed-compute step on an experts module instance (fused_int4.py:262);
+    ``jtopk`` as in make_experts_forward."""
     _check_silu(experts)
     _check_dtype(experts, "experts")
     for name in ("gate_up_proj", "down_proj"):
         experts._parameters.pop(name, None)
-    experts.forward = types.MethodType(make_experts_forward(store), experts)
+    experts.forward = types.MethodType(make_experts_forward(store, jtopk), experts)
     experts._tmoe_store = store
     return experts
 

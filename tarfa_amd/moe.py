@@ -220,6 +220,21 @@ def dispatch(ids, num_experts, workspace: Workspace):
     return offsets, perm, inv
 
 
+def topk_renorm(ids, weights, j):
+    """The reference's re-truncation of a routing to j experts (tarfa/engine/fused_int4.py:157-160):
+    per token the j largest bf16 weights (equal weights keep the lower slot first), their ids,
+    and the weights renormalised in bf16; returns (ids [T,j] int64, weights [T,j] bf16)."""
+    dev = ids.device
+    T, k = ids.shape
+    _need(ids, "top_k_index", torch.int64, (T, k), dev)
+    _need(weights, "top_k_weights", torch.bfloat16, (T, k), dev)
+    ids_out = torch.empty(T, j, dtype=torch.int64, device=dev)
+    w_out = torch.empty(T, j, dtype=torch.bfloat16, device=dev)
+    check(lib().tmoe_topk_renorm_bf16(_p(ids), _p(weights), T, k, j, _p(ids_out), _p(w_out), _stream(dev)),
+          "tmoe_topk_renorm_bf16")
+    return ids_out, w_out
+
+
 def experts_forward(shape: MoEShape, x, ids, weights, table, workspace: Workspace, out=None):
     """Routed experts only (the reference's experts.forward); returns out [T,H] bf16.
 

@@ -74,6 +74,45 @@ def test_install_experts_on_a_transformers_block(gpu, T):
     assert out.data_ptr() != x.data_ptr()
 
 
+@pytest.mark.parametrize("T,k,j,ties", [(1, 8, 5, False), (37, 8, 5, True), (1000, 8, 1, False), (64, 16, 8, True),
+                                       (5, 8, 8, False)])
+def test_topk_renorm_matches_the_oracle(gpu, T, k, j, ties):
+    """tmoe_topk_renorm_bf16 (fused_int4.py:157-160) bit-exact against the oracle's restatement,
+    ties (equal weights keep the lower slot) included."""
+    g = np.random.default_rng(T * 7 + k + j)
+    vals = np.array([0.125, 0.25, 0.5], np.float32) if ties else None
+    w = (g.choice(vals, (T, k)) if ties else bf16.rnd(g.uniform(0.01, 1.0, (T, k)).astype(np.float32)))
+    ids = g.integers(0, 257, (T, k))
+    ti = torch.from_numpy(ids).to(gpu)
+    tw = torch.from_numpy(w.astype(np.float32)).to(BF).to(gpu)
+    got_ids, got_w = tm.topk_renorm(ti, tw, j)
+    want_ids, want_w = moe.jtopk_truncate(ids, w, j) if j < k else (ids, w)
+    if j == k:                                           # nothing to cut: still the renormalised weights
+        want_ids, want_w = moe.jtopk_truncate(np.pad(ids, ((0, 0), (0, 1))), np.pad(w, ((0, 0), (0, 1))), j)
+    assert np.array_equal(got_ids.cpu().numpy(), want_ids)
+    assert np.array_equal(f32(got_w), want_w)
+
+
+@pytest.mark.parametrize("T", [1, 17])
+def test_install_experts_cuts_the_routing_to_jtopk(gpu, T, monkeypatch):
+    """The reference's JTOPK (environment, fused_int4.py:17) below the router's top-k: the routed
+    step runs on the top-JTOPK weights renormalised, as fused_int4.py:157-160 does."""
+    monkeypatch.setenv("JTOPK", "5")
+    blk, layer = _tf_block(SHAPE, 80 + T, gpu)
+    ex = blk.experts
+    store = tx.ExpertStore.from_slabs(SHAPE, ex.gate_up_proj.data, ex.down_proj.data)
+    tx.install_experts(ex, store)
+    x = seeded.make_tokens(SHAPE, 80 + T, T, device=gpu)
+    with torch.no_grad():
+        out = blk(x.reshape(1, T, -1)).reshape(T, -1)
+        _, tw, ti = blk.gate(x)
+    torch.cuda.synchronize()
+    store.check_status()
+    ids5, w5 = moe.jtopk_truncate(ti.cpu().numpy(), f32(tw), 5)
+    ref = _oracle_block(x, ids5, w5, layer, SHAPE)
+    assert_close_bf16(f32(out), ref, f"JTOPK=5 T={T}")
+
+
 @pytest.mark.parametrize("T", [1, 17])
 def test_from_transformers_block(gpu, T):
     blk, layer = _tf_block(SHAPE, 60 + T, gpu)

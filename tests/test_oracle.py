@@ -144,6 +144,37 @@ def test_router_tie_breaks_to_lower_index():
     assert ids.tolist() == [[1, 2, 4]]
 
 
+@pytest.mark.parametrize("k,j", [(8, 5), (8, 1), (16, 8), (6, 4)])
+def test_jtopk_truncate_matches_the_reference_lines_in_torch(k, j):
+    """fused_int4.py:157-160 run in torch CPU bf16 (topk, gather, sum, divide) on untied weights
+    whose kept values span few binades (the fp32 sum is then exact, so its order is moot)."""
+    g = np.random.default_rng(k * 31 + j)
+    for trial in range(50):
+        w = bf16.rnd(g.uniform(0.02, 1.0, (7, k)).astype(np.float32))
+        if any(len(set(r.tolist())) < k for r in w):
+            continue                                    # torch's tie order is not defined
+        ids = g.integers(0, 256, (7, k))
+        tw, tid = tb(w), torch.from_numpy(ids)
+        tv, ti = tw.topk(j, dim=-1)
+        want_ids = torch.gather(tid, -1, ti)
+        want_w = tv / tv.sum(dim=-1, keepdim=True)
+        got_ids, got_w = moe.jtopk_truncate(ids, w, j)
+        assert np.array_equal(got_ids, want_ids.numpy())
+        assert np.array_equal(got_w, want_w.float().numpy())
+
+
+def test_jtopk_truncate_ties_keep_the_lower_slot_and_passes_short_routings():
+    w = bf16.rnd(np.array([[0.25, 0.5, 0.25, 0.5, 0.125, 0.25]], np.float32))
+    ids = np.array([[10, 11, 12, 13, 14, 15]])
+    got_ids, got_w = moe.jtopk_truncate(ids, w, 4)
+    assert got_ids.tolist() == [[11, 13, 10, 12]]       # 0.5 (slots 1, 3), then 0.25 (slots 0, 2)
+    s = bf16.rnd(np.float32(1.5))
+    half, quarter = (np.asarray(bf16.rnd(np.float32(v) / s)).item() for v in (0.5, 0.25))
+    assert got_w.tolist() == [[half] * 2 + [quarter] * 2]
+    same_ids, same_w = moe.jtopk_truncate(ids, w, 6)   # k <= j: the routing is kept as it is
+    assert np.array_equal(same_ids, ids) and np.array_equal(same_w, w)
+
+
 # ------------------------------------------------------------------ dispatch
 
 @pytest.mark.parametrize("T,k,E", [(1, 8, 32), (2, 2, 4), (7, 3, 5), (33, 8, 32), (64, 1, 16)])
