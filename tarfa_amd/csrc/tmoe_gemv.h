@@ -244,7 +244,7 @@ __device__ __forceinline__ void wave_topk_select(const float* src, int E, int k,
   wave_topk_values<MAXEPL, MAXK>(v, E, k, lane, id, w);
 }
 
-// E <= 256 logits (4 per lane), k <= 8: the bitonic selection of tmoe_topk.h (lane r < k
+// E <= 256 logits (4 per lane), k <= 8: the round selection of tmoe_topk.h (lane r < k
 // gets slot r), then the softmax and renormalisation of wave_topk_values with the same
 // operations in the same order (the denominator a wave sum, the renormalising sum over
 // slots 0 .. k-1 in order), so ids and weights are bit-identical to the k-round selection;
@@ -260,7 +260,7 @@ __device__ __forceinline__ void wave_topk8(const float* src, bool coherent, int 
   }
   int id = E;
   float lw = -INFINITY, top = 0.f;
-  top8_bitonic(v, E, k, lane, id, lw, top);
+  top8_rounds(v, E, k, lane, id, lw, top);
   // The largest logit (slot 0's), -inf when nothing is selectable.
   const bool any = __builtin_amdgcn_readfirstlane(id) != E;
   const float m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(any ? lw : -INFINITY)));

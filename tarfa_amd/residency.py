@@ -168,6 +168,8 @@ class ResidencyLedger:
 
     def load_layer(self, layer, parts):
         """Copy a layer's experts from full tensors ([E, ...] per part, any device)."""
+        if self.tiered:
+            torch.cuda.synchronize(self.device)      # the host tier is written by the CPU: no kernel may be reading it
         self._store(layer, 0, [p.to(self.device) if not self.tiered else p for p in parts])
         torch.cuda.synchronize(self.device)
 
@@ -196,6 +198,10 @@ class ResidencyLedger:
         side = self._side_stream()
         side.wait_stream(torch.cuda.current_stream(dev))
         if self.tiered:
+            # The CPU writes the pinned host tier directly, and kernels already queued on any
+            # stream may still read it (non-resident experts), as may an earlier side-stream
+            # copy into the HBM slots: wait for all of them before the first write.
+            torch.cuda.synchronize(dev)
             for l, jl in enumerate(src):
                 jnf.read_experts(jl, range(E), self.host[l][0], self.host[l][1], verify=verify)
                 with torch.cuda.stream(side):

@@ -57,13 +57,14 @@ def test_small_batch_block_full_size(gpu, T):
     _block_case(FULL, T, 400 + T, gpu)
 
 
-def test_small_batch_router_weights_path(gpu):
-    """Router logits computed on the device (fp32 GEMV) before the small-batch experts."""
-    shape, T = MID, 6
-    layer = seeded.make_layer(shape, 77, device=gpu)
+@pytest.mark.parametrize("shape,T,seed", [(MID, 6, 77), (FULL, 2, 78), (FULL, 16, 79)])
+def test_small_batch_router_weights_path(gpu, shape, T, seed):
+    """Router logits computed on the device (fp32 GEMV) before the small-batch experts, at the
+    mid shape and at the full-size layer (H=2560, E=256) for the smallest and largest T."""
+    layer = seeded.make_layer(shape, seed, device=gpu)
     ws = Workspace(shape, gpu, tokens=T)
     table = tm.expert_table(layer.gate_up, layer.down)
-    x = seeded.make_tokens(shape, 77, T, device=gpu)
+    x = seeded.make_tokens(shape, seed, T, device=gpu)
     out, ids, w = tm.moe_block(shape, x, table, ws, router_w=layer.router_w, shared=layer.shared)
     torch.cuda.synchronize()
     xs = f32(x)
@@ -75,7 +76,7 @@ def test_small_batch_router_weights_path(gpu):
     gu, dn = expert_dicts(layer.gate_up, layer.down, ids_ref)
     ref = moe.add_bf16(moe.experts_prefill(xs, ids_ref, f32(w), gu, dn, shape.num_experts),
                        moe.shared_expert(xs, *[f32(t) for t in layer.shared]))
-    assert_close_bf16(f32(out), ref, "small-batch block, device router")
+    assert_close_bf16(f32(out), ref, f"small-batch block, device router, H={shape.hidden} T={T}")
 
 
 def test_small_batch_duplicates_sentinel_hot_expert(gpu):
