@@ -237,7 +237,7 @@ int tmoe_moe_layer_int4(const void* h, int T, const void* ln_w, float eps, const
  * device array inside the library, TMOE_STATIC_SCRATCH_BYTES per GPU, held by each GPU
  * the library runs on until the process ends.  Nothing is allocated by the call.
  *   - Calls needing a larger workspace than the static one (tmoe_workspace_bytes(T, ...)
- *     > TMOE_STATIC_SCRATCH_BYTES; at H=2560, E=256, I=Is=1024, k=8 that is T > 220)
+ *     > TMOE_STATIC_SCRATCH_BYTES; at H=2560, E=256, I=Is=1024, k=8 that is T > 219)
  *     return TMOE_ERR_SCRATCH before any launch.
  *   - `status`: a caller-owned device uint32 (4-byte aligned, required) into which the
  *     kernels OR device-detected conditions: 1 = an expert id outside [0, E] (cannot come
