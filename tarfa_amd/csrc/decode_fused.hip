@@ -435,7 +435,9 @@ __device__ __forceinline__ void resolve_block(const DecodeParams& p, int lane, u
   if (!p.logits_in) {
     // Every load of a poll round is issued before any is waited for: the
     // addresses are clamped into the logit words, never skipped.  The shared-gate
-    // logit is not waited for here: only the combine needs it.
+    // logit is not waited for here: only the combine needs it.  (Two rounds in flight,
+    // the second half a round trip behind, saw the logits later, not sooner: 6.5-7.8
+    // against 5.0-5.7 us in the timeline, with two to three times the rounds.)
     Backoff<1> b;
     for (;;) {
       uint64_t w[MAXEPL];
@@ -658,15 +660,28 @@ __device__ __forceinline__ void task_router(const DecodeParams& p, int t, int la
   }
 }
 
+// The words a D(k-1) task combines (lane r < 8: its row h0 + r of each earlier slot, then
+// of the shared expert; clamped addresses), one batch of loads after the task's own rows.
+// (Requested before the rows, to overlap the round trip, they cost the exact-bf16 call
+// 0.2-0.5 us in a same-run A/B, while the int4 mode, whose down tasks are shorter, gains
+// 0.8 us that way: combine_words_q4.)
+__device__ __forceinline__ void combine_words(const DecodeParams& p, int h0, int lane, uint64_t (&v)[kFusedMaxK]) {
+  const int r = lane & (kDownRows - 1);
+#pragma unroll
+  for (int j = 0; j < kFusedMaxK; ++j) {
+    const int slot = j < p.k - 1 ? j : p.k;
+    v[j] = ld64c(p.dq64 + ((size_t)slot * p.H + h0 + r) / 2);
+  }
+}
+
 // A D(k-1) task: combine rows h0..h0+7 from every slot's tagged down results (its
 // own in registers) and write the output.  The routing comes from the wave's
-// cache.  Lane r < 8 owns row h0 + r: it reads the word holding that row for each
-// earlier slot and the shared expert (one batch of loads, clamped addresses),
-// then folds in router order, acc = bf16(acc + bf16(w_j * d_j)), and adds
-// bf16(gate * d_shared).
+// cache.  Lane r < 8 owns row h0 + r: it checks the words of combine_words (pre),
+// re-reading them while any still carries an old tag, then folds in router order,
+// acc = bf16(acc + bf16(w_j * d_j)), and adds bf16(gate * d_shared).
 __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, int h0, int lane,
                                              const float (&d_last)[kDownRows], uint32_t& rwc, uint32_t tag,
-                                             uint32_t* err, RouteLds& L) {
+                                             uint32_t* err, RouteLds& L, const uint64_t (&pre)[kFusedMaxK]) {
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
   const int r = lane & (kDownRows - 1);
@@ -676,13 +691,10 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
   // shared expert (slot k); words past that are never used.
   uint32_t pr[kFusedMaxK];
   Backoff<4> b;
-  for (;;) {
-    uint64_t v[kFusedMaxK];
+  uint64_t v[kFusedMaxK];
 #pragma unroll
-    for (int j = 0; j < kFusedMaxK; ++j) {
-      const int slot = j < k - 1 ? j : k;
-      v[j] = ld64c(p.dq64 + ((size_t)slot * p.H + h0 + r) / 2);
-    }
+  for (int j = 0; j < kFusedMaxK; ++j) v[j] = pre[j];
+  for (;;) {
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < kFusedMaxK; ++j) {
@@ -692,6 +704,7 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
     }
     if (__all(ok)) break;
     if (!b.step(err)) break;
+    combine_words(p, h0, lane, v);
   }
   // Lane r < 8 takes its own row of this slot (the row values are wave-uniform).
   static_assert(kDownRows == 8, "one row per lane of lanes 0..7");
@@ -722,6 +735,19 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
   if (lane < kDownRows) p.out[h0 + lane] = f32_to_bf16(acc);
 }
 
+// Int4 mode: the words the last slot's task combines, one fp32 row per word, requested
+// before the task's own rows and scales: the other slots' down tasks for these rows were
+// queued long before, so the words have usually landed when the combine reads them and it
+// costs no round trip of its own at the end of the call (30.4-30.6 -> 29.5-29.9 us).
+template <int RQ>
+__device__ __forceinline__ void combine_words_q4(const DecodeParams& p, int h0, int lane, uint64_t (&v)[kFusedMaxK]) {
+  const int r = lane & (RQ - 1);
+#pragma unroll
+  for (int j = 0; j < kFusedMaxK; ++j) {
+    const int slot = j < p.k - 1 ? j : p.k;
+    v[j] = ld64c(p.dq64 + (size_t)slot * p.H + h0 + r);
+  }
+}
 // Int4 mode: the combine of rows h0 .. h0 + RQ - 1 (lane r < RQ owns row h0 + r).
 // Each slot's fp32 row is weighted and summed in fp32 in router order,
 // y = y + w_j * d_j with separately rounded products and sums (the reference's
@@ -730,7 +756,7 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int e_last, 
 template <int RQ>
 __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, int h0, int lane,
                                            const float (&d_last)[RQ], uint32_t& rwc, uint32_t tag, uint32_t* err,
-                                           RouteLds& L) {
+                                           RouteLds& L, const uint64_t (&pre)[kFusedMaxK]) {
   const int k = p.k;
   const bool has_sh = p.sh_gate != nullptr;
   const int r = lane & (RQ - 1);
@@ -738,13 +764,10 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
   const float hres = p.resid ? bf16_to_f32(p.resid[h0 + r]) : 0.f;
   uint32_t pr[kFusedMaxK];   // word j: this lane's row of slot j (j < k - 1) or of the shared expert (j = k - 1)
   Backoff<4> b;
-  for (;;) {
-    uint64_t v[kFusedMaxK];
+  uint64_t v[kFusedMaxK];
 #pragma unroll
-    for (int j = 0; j < kFusedMaxK; ++j) {
-      const int slot = j < k - 1 ? j : k;
-      v[j] = ld64c(p.dq64 + (size_t)slot * p.H + h0 + r);
-    }
+  for (int j = 0; j < kFusedMaxK; ++j) v[j] = pre[j];
+  for (;;) {
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < kFusedMaxK; ++j) {
@@ -754,6 +777,7 @@ __device__ __forceinline__ void combine_q4(const DecodeParams& p, int e_last, in
     }
     if (__all(ok)) break;
     if (!b.step(err)) break;
+    combine_words_q4<RQ>(p, h0, lane, v);
   }
   int rows[RQ];
 #pragma unroll
@@ -792,6 +816,8 @@ __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, in
   float d[RQ];
 #pragma unroll
   for (int r = 0; r < RQ; ++r) d[r] = 0.f;
+  uint64_t pre[kFusedMaxK];   // the last slot's combine words, requested before the rows (see combine_words)
+  if (slot == p.k - 1) combine_words_q4<RQ>(p, h0, lane, pre);
   if (e >= 0)
     down_q4<MI, RQ, QR>(reinterpret_cast<const uint8_t*>(ld_inv(p.table + 4 * e + 2)),
                     reinterpret_cast<const uint16_t*>(ld_inv(p.table + 4 * e + 3)), p.act64 + (size_t)slot * p.I / 2,
@@ -804,7 +830,7 @@ __device__ __forceinline__ void task_down_q4(const DecodeParams& p, int slot, in
     const int row = spread(rows);
     if (lane < RQ) st64c(p.dq64 + (size_t)slot * p.H + h0 + lane, tagged(tag, (uint32_t)row));
   } else {
-    combine_q4<RQ>(p, e, h0, lane, d, rwc, tag, err, L);
+    combine_q4<RQ>(p, e, h0, lane, d, rwc, tag, err, L, pre);
   }
 }
 
@@ -1051,6 +1077,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       const int e = shared ? 0 : wave_slot_expert(p, tk.slot, rwc);
       const int h0 = tk.idx * kDownRows;
       float d[kDownRows] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      uint64_t pre[kFusedMaxK];
       if (e >= 0) {
         const uint16_t* w = shared ? p.sh_down : reinterpret_cast<const uint16_t*>(ld_inv(p.table + 2 * e + 1));
         const uint64_t* a = p.act64 + (shared ? (size_t)p.k * p.I / 2 : (size_t)tk.slot * p.I / 2);
@@ -1075,7 +1102,8 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
         if (lane < kDownRows / 2)
           st64c(p.dq64 + ((size_t)(shared ? p.k : tk.slot) * p.H + h0) / 2 + lane, tagged(tag, (uint32_t)pair));
       } else {
-        combine_rows(p, e, h0, lane, d, rwc, tag, err, s_rt);
+        combine_words(p, h0, lane, pre);
+        combine_rows(p, e, h0, lane, d, rwc, tag, err, s_rt, pre);
       }
     }
     if (!got) {
