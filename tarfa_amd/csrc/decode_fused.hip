@@ -975,16 +975,18 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       load_xpack<MH, EXACT>(xf, p.x, p.H, lane);
     }
   };
-  // Waves whose first task is not a router task form x at once: most of them next wait for
-  // the routing, which this overlaps (router waves form it inside their task instead,
-  // behind their rows' loads).
+  uint32_t ticket = DYN ? (uint32_t)__builtin_amdgcn_readlane((int)first, 0) : rank;
+  // Waves whose first task (the drawn ticket's) is not a router task form x at once: most of
+  // them next wait for the routing, which this overlaps (router waves form it inside their
+  // task instead, behind their rows' loads).  Deciding by the block's rank instead, as with
+  // static tickets, left the waves that drew another wave's planned router task to form x on
+  // first use: 39.1-39.2 against 37.9-38.2 us per layer.
   if constexpr (LN) {
-    if (q + NQ * (int)rank >= p.n_r) {
+    if (q + NQ * (int)ticket >= p.n_r) {
       load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane0);
       have_x = true;
     }
   }
-  uint32_t ticket = DYN ? (uint32_t)__builtin_amdgcn_readlane((int)first, 0) : rank;
   const uint64_t t_entry = p.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
   if (p.trace && blockIdx.x == 0 && wid == 0 && lane0 == 0) {
     const uint64_t hdr[kTraceHeader] = {(uint64_t)p.n_tasks, gridDim.x, (uint64_t)p.n_r, (uint64_t)p.n_s,
