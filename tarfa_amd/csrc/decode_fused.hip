@@ -85,7 +85,10 @@ constexpr int q4_down_rows(int MI) { return MI <= 2 ? 16 : 8; }
 constexpr int kFusedMaxK = 8;          // top-k handled by the fused kernel (larger k takes the unfused path)
 constexpr int kDownLag = 8;            // Dj is queued after G(j + kDownLag): with k <= 8, every D after every G
 constexpr int kSharedAfter = 1;        // the shared gate/up tasks are queued after this slot's gate/up tasks
-constexpr int kSharedDelay = 64;       // exact-bf16: the shared gate/up tasks' start delay, x 64 cycles (~2 us)
+// The shared gate/up tasks' start delay, x 64 cycles: exact bf16 ~2 us; int4 ~3 us (int4 at the
+// full-size layer: 32 -> 29.5-29.9 us, 64 -> 28.9-29.1, 100 -> 28.4-28.5, 127 -> 29.0-29.2).
+template <bool Q4>
+constexpr int shared_delay() { return Q4 ? 100 : 64; }
 // Tickets: every one drawn from a per-queue counter, in both modes, so the call completes
 // whatever subset of the grid is resident (the int4 mode's short tasks hide less of the draw's
 // round trip than the exact-bf16 ones, but static tickets would need the whole grid resident).
@@ -1042,15 +1045,12 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
       }
       if (tk.idx == 0) publish_routing(p, lane, rwc);
     }
-    // Exact-bf16 mode: the shared gate/up tasks (all drawn at entry) issue their loads ~2 us
-    // late.  Issued at once, their 10.5 MB sits in the memory queues in front of the router
-    // rows loaded beside them, and the routing is the critical path; the shared expert has
-    // slack until the routing resolves (~8 us).  36.4 -> 35.3 us at the full-size layer.  Int4
-    // mode keeps them at once: its S waves take the last gate/up tasks next (25.2 -> 26.2 us
-    // with the delay).
-    if constexpr (!Q4) {
-      if (tk.type == kTS && i == 0) __builtin_amdgcn_s_sleep(kSharedDelay);
-    }
+    // The shared gate/up tasks (all drawn at entry) issue their loads a few us late.  Issued at
+    // once, their rows sit in the memory queues in front of the router rows loaded beside them,
+    // and the routing is the critical path; the shared expert has slack until the routing
+    // resolves (~8 us).  Exact bf16 36.4 -> 35.3 us at the full-size layer; int4 (now that its
+    // tickets are drawn too) 29.6-29.7 -> 28.4-28.5 us.
+    if (tk.type == kTS && i == 0) __builtin_amdgcn_s_sleep(shared_delay<Q4>());
     if (tk.type == kTR) {
       task_router<MH, EXACT, LN>(p, tk.idx, lane, get_x, tag, take);
     } else if (tk.type == kTS || tk.type == kTG) {
