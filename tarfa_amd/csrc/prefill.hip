@@ -555,6 +555,13 @@ __device__ __forceinline__ void dsw16(uint32_t lds, const u32x4& v) {
   asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(lds), "v"(v), "n"(OFS) : "memory");
 }
 
+// s_waitcnt vmcnt(N) with four registers passed through it (nothing reads them before).
+template <int N, typename T>
+__device__ __forceinline__ void wait_vm_regs(T& a, T& b, T& c, T& d) {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+
 // One wave's view of one tile (all wave-uniform).
 struct PTile {
   int arow0;                // A row of the tile's first row (gather: its position in perm)
@@ -766,6 +773,58 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
       }
     }
   };
+  // Int4: one k step's MFMAs with the next k step's dequantisation woven between them.  An
+  // MFMA keeps the matrix unit busy 16 cycles, in which the wave issues independent VALU
+  // work, so the dequantisation (~3 VALU instructions per MFMA) need not sit between the
+  // weight load and the MFMAs.  Group i: its token block's MFMAs, one piece of the next
+  // fragments (group 0: the nibble planes and scales; groups 1..8: one 32-bit word of the
+  // two fragments each), and the A fragment read two blocks ahead; sched_barrier keeps the
+  // groups in this order.  cur: this k step's fragments; next k step: stage nu, step nks.
+  // The dequantised values are dequant_frag's, bit for bit.
+  auto mma_q4 = [&](int u, int ks, const u32x4 (&cur_b)[kPNB], int nu, int nks, u32x4 (&nxt_b)[kPNB]) {
+    const u32x4* lh = slots[u] + (ks ? a_rd1 : a_rd0);
+    const int ns = nu % kPB;
+    bf16x8_t bc[kPNB];
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) bc[nb] = as_bf16x8(cur_b[nb]);
+    uint32_t lo[kPNB], hi[kPNB];
+    float sc[kPNB], m8[kPNB];
+    bf16x8_t a0 = as_bf16x8(lh[0]), a1 = as_bf16x8(lh[128]);
+#pragma unroll
+    for (int i = 0; i < kPMB; ++i) {
+      const bf16x8_t a = a0;
+      a0 = a1;
+      if (i + 2 < kPMB) a1 = as_bf16x8(lh[(i + 2) * 128]);
+#pragma unroll
+      for (int nb = 0; nb < kPNB; ++nb)
+        acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bc[nb], acc[i][nb], 0, 0, 0);
+      if (i == 0) {
+#pragma unroll
+        for (int nb = 0; nb < kPNB; ++nb) {
+          const uint32_t q = qreg[ns][nb][nks];
+          lo[nb] = q & 0x0F0F0F0Fu;
+          hi[nb] = (q >> 4) & 0x0F0F0F0Fu;
+          asm volatile("" : "+v"(lo[nb]), "+v"(hi[nb]));   // keep the byte planes: one conversion per value
+          const uint32_t sr = sreg[ns][nb];
+          const uint32_t bits = ((nu >> 1) & 1) ? (sr & 0xFFFF0000u) : (sr << 16);
+          sc[nb] = QR ? scale_f32<true>((uint16_t)sr) : __uint_as_float(bits);
+          m8[nb] = -8.0f * sc[nb];
+        }
+      } else if (i <= 4 * kPNB) {
+        const int w = i - 1, nb = w / 4, b = w % 4;
+        const float e = fmaf((float)((lo[nb] >> (8 * b)) & 0xFFu), sc[nb], m8[nb]);
+        const float o = fmaf((float)((hi[nb] >> (8 * b)) & 0xFFu), sc[nb], m8[nb]);
+        const bf16x2_t v = {(__bf16)e, (__bf16)o};   // (even k low, odd k high)
+        const uint32_t d = __builtin_bit_cast(uint32_t, v);
+        if (b == 0) nxt_b[nb].x = d;
+        else if (b == 1) nxt_b[nb].y = d;
+        else if (b == 2) nxt_b[nb].z = d;
+        else nxt_b[nb].w = d;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  static_assert(!Q4 || 4 * kPNB + 1 <= kPMB, "every word of the next fragments has a group");
   // Each stage ends with this wave's A loads of the next stage landed (everything but the
   // last kPA - 1 stages' loads done: exact while only loads are outstanding, stricter right
   // after an epilogue's stores) and a raw barrier: every wave's part of the next A stage is
@@ -851,6 +910,19 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
     if (v >= kPR - kPB) load_b(v - (kPR - kPB), false, v - (kPR - kPB));
   }
   stage_end();
+  // Int4: stage 0's B loads landed (the kPB - 1 later B stages and their A loads may still be
+  // in flight) and its first k step's fragments formed; every later stage finds its first
+  // fragments formed during the previous stage's second k step.
+  u32x4 bq4[kPNB];
+  if constexpr (Q4) {
+    wait_vm_regs<(kPB - 1) * kOpsPerStage>(qreg[0][0][0], qreg[0][0][1], qreg[0][1][0], qreg[0][1][1]);
+    asm volatile("" : "+v"(sreg[0][0]), "+v"(sreg[0][1]));
+#pragma unroll
+    for (int nb = 0; nb < kPNB; ++nb) {
+      const uint32_t sr = sreg[0][nb];
+      bq4[nb] = dequant_frag(qreg[0][nb][0], QR ? scale_f32<true>((uint16_t)sr) : __uint_as_float(sr << 16));
+    }
+  }
   // Stage st of tile j (A slot st % kPR, B slot st % kPB): refill the A slot read at the
   // previous stage with stage st + kPA, multiply, refill this stage's B slot with stage
   // st + kPB; stages past the tile's end are the next tile's first ones (for the last
@@ -863,8 +935,22 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
       const int sa = st0 + u + kPA, sb = st0 + u + kPB;
       const bool na = kTail && u + kPA >= kPR, nb = kTail && u + kPB >= kPR;   // past the tile's end
       dma_a((u + kPA) % kPR, na, na ? sa - nk : sa);
-      wait_b(u % kPB);
-      multiply(u);
+      if constexpr (Q4) {
+        // k step 0 (fragments formed before) forming k step 1's; then, once stage u + 1's B
+        // loads have landed (issued kPB - 1 stages ago: only the kPB - 2 later B stages with
+        // their A loads and this stage's A loads may still be outstanding), k step 1 forming
+        // stage u + 1's first.
+        u32x4 q1[kPNB];
+        mma_q4(u, 0, bq4, u, 1, q1);
+        const int n1 = (u + 1) % kPB;
+        wait_vm_regs<(kPB - 2) * kOpsPerStage + kPLoads>(qreg[n1][0][0], qreg[n1][0][1], qreg[n1][1][0],
+                                                            qreg[n1][1][1]);
+        asm volatile("" : "+v"(sreg[n1][0]), "+v"(sreg[n1][1]));
+        mma_q4(u, 1, q1, u + 1, 0, bq4);
+      } else {
+        wait_b(u % kPB);
+        multiply(u);
+      }
       load_b(u % kPB, nb, nb ? sb - nk : sb);
       stage_end();
     }
