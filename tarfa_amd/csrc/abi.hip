@@ -24,9 +24,10 @@ bool sb_supported(int T, int H, int I, int Is, int k, int q4);
 int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
               const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
               const uint16_t* sh_down, const uint16_t* sh_gate_w, int H, int E, int I, int k, int Is,
-              uint16_t* out, void* ws, hipStream_t s, const uint16_t* resid, uint32_t* err);
+              uint16_t* out, void* ws, hipStream_t s, const uint16_t* resid, uint32_t* err, int sh_pre);
 int sb_router_launch(const uint16_t* x, const uint16_t* wg, int T, int H, int E, int I, int k, int Is,
-                     int64_t* ids64, uint16_t* wb, uint32_t* heat, void* ws, hipStream_t s);
+                     const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_gate_w, int64_t* ids64,
+                     uint16_t* wb, uint32_t* heat, void* ws, hipStream_t s, int* sh_pre);
 }  // namespace tmoe
 
 
@@ -146,7 +147,7 @@ static int experts_forward(const void* x, int T, const int64_t* ids, const void*
   }
   if (small_batch(T, H, I, 0, k, q4))
     return sb_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table, nullptr,
-                     nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, nullptr, nullptr);
+                     nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, nullptr, nullptr, 0);
   return prefill_launch((const uint16_t*)x, T, nullptr, ids, nullptr, (const uint16_t*)weights, expert_table,
                         nullptr, nullptr, nullptr, nullptr, H, E, I, k, 0, (uint16_t*)out, workspace, s, q4, nullptr,
                         nullptr);
@@ -239,18 +240,20 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
   float* wf = ws_ptr<float>(workspace, L.wts);
   float* gs = ws_ptr<float>(workspace, L.gs);
   if (small_batch(T, H, I, Is, k, q4)) {
-    // Router (logits and top-k in one launch), then the small-batch experts; the shared gate
-    // is computed inside.
+    // Router (logits and top-k in one launch, with the shared expert's gate/up beside it), then
+    // the small-batch experts; the shared gate is computed inside.
+    int sh_pre = 0;
     if (logits_in) {
       if (int st = launch_router_topk(logits_in, T, E, k, ids_out, (uint16_t*)weights_out, ids32, wf, heat, s))
         return st;
-    } else if (int st = sb_router_launch((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, I, k, Is, ids_out,
-                                         (uint16_t*)weights_out, heat, workspace, s)) {
+    } else if (int st = sb_router_launch((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, I, k, Is,
+                                         (const uint16_t*)sh_gate, (const uint16_t*)sh_up, (const uint16_t*)sh_gate_w,
+                                         ids_out, (uint16_t*)weights_out, heat, workspace, s, &sh_pre)) {
       return st;
     }
     return sb_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
                      (const uint16_t*)sh_up, (const uint16_t*)sh_down, (const uint16_t*)sh_gate_w, H, E, I, k, Is,
-                     (uint16_t*)out, workspace, s, ln_w ? (const uint16_t*)h : nullptr, err);
+                     (uint16_t*)out, workspace, s, ln_w ? (const uint16_t*)h : nullptr, err, sh_pre);
   }
   const float* lg = logits_in;
   if (!lg) {

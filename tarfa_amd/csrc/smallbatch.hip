@@ -91,6 +91,8 @@ struct SbParams {
   struct SbSlice* slices;     // [1 + kSbMaxEntries + 2] header (slice count), then the down kernel's slices
   uint32_t* err;
   uint16_t* out;              // [T, H]
+  int sh_pre;                 // 1: the shared expert's gate/up and gate ran in the router launch, its down
+                              // runs in the up launch (the down launch's slices are the routed ones)
 };
 
 struct SbGroups {
@@ -122,7 +124,7 @@ __device__ __forceinline__ int sb_group_of(const SbGroups& g, int e) {
 }
 
 // Groups and slices from the ids (T*k <= 256; any block of at least 64 threads).
-__device__ void sb_groups(const SbParams& p, SbGroups& g) {
+__device__ void sb_groups(const SbParams& p, SbGroups& g, bool duty) {
   const int tid = threadIdx.x, nthr = blockDim.x, n = p.T * p.k;
   for (int j = tid; j < 32; j += nthr) g.present[j] = 0u;
   for (int j = tid; j < 256; j += nthr) g.gmask[j] = 0u;
@@ -146,7 +148,7 @@ __device__ void sb_groups(const SbParams& p, SbGroups& g) {
     // The expert's gate_up rows, requested now: the round trip overlaps the group work below.
     ew[i] = e >= 0 ? reinterpret_cast<const uint16_t*>(p.table[2 * e]) : nullptr;
   }
-  if (bad && blockIdx.x == 0) atomicOr(p.err, (uint32_t)kErrExpertId);
+  if (bad && duty) atomicOr(p.err, (uint32_t)kErrExpertId);
   __syncthreads();
   for (int j = tid; j < n; j += nthr) {
     const int e = g.ids[j];
@@ -232,7 +234,7 @@ __device__ __forceinline__ void sb_tokens(SbGroups& g, uint32_t mask, int r0, in
 // The down kernel's slice descriptors (block 0 of the up kernel).
 __device__ void sb_slices(const SbParams& p, const SbGroups& g) {
   const int T = p.T, I = p.I;
-  const int nshs = p.sh_gate ? (T + kSbSlice - 1) / kSbSlice : 0;
+  const int nshs = p.sh_gate && !p.sh_pre ? (T + kSbSlice - 1) / kSbSlice : 0;
   const int total = nshs + g.NS;
   for (int si = threadIdx.x; si < total; si += blockDim.x) {
     SbSlice d;
@@ -369,51 +371,15 @@ __device__ void sb_combine(const SbParams& p, const SbOrder& o, int c0, int ncol
   }
 }
 
-// Up: one wave per (slice, 8 activation columns) = 8 gate and 8 up weight rows over K = H
-// (128 nkb columns, R stages in flight); block 0 also writes the combine order and the down
-// kernel's slice descriptors; blocks 0 .. T-1 (shared slice 0) compute the shared gate.
+// Up work of one (slice, 8 activation columns) tile: 8 gate and 8 up weight rows over K = H
+// (H / 128 stages, R in flight), act = bf16(bf16(silu(bf16 g)) * bf16 u) for the slice's ms
+// token rows into the activations at arow0.  The lane's A rows: tok[j] = the token of slice
+// row min(4 j + lane / 16, ms - 1).  bt, at: the wave's LDS.
 template <int R>
-__global__ __launch_bounds__(64) void k_sb_up(SbParams p) {
-  __shared__ SbGroups g;
-  __shared__ u32x4 bt[16 * 17];                       // a stage's 16 weight rows x 16 chunks, rows padded
-  __shared__ u32x4 at[8 * 17];                        // a stage's token rows x 16 chunks, rows padded
-  sb_groups(p, g);
-  if (blockIdx.x == 0) {
-    sb_order(p, g);
-    sb_slices(p, g);
-  }
+__device__ __forceinline__ void sb_up_tile(const SbParams& p, const uint16_t* gate, const uint16_t* up, int tile,
+                                           size_t arow0, int ms, const int (&tok)[2], u32x4* bt, u32x4* at) {
   const int lane = threadIdx.x;
-  const int T = p.T, H = p.H, I = p.I;
-  const int tiles = I / 8;
-  const int nshs = p.sh_gate ? (T + kSbSlice - 1) / kSbSlice : 0;
-  const int nkb = H / 128;
-  int b = blockIdx.x, tile, sj, ms;
-  uint32_t mask;
-  size_t arow0;
-  const uint16_t *gate, *up;
-  const bool shared = b < nshs * tiles;
-  if (shared) {
-    sj = b / tiles;
-    tile = b - sj * tiles;
-    mask = (1u << T) - 1u;
-    ms = min(kSbSlice, T - kSbSlice * sj);
-    arow0 = (size_t)(T * p.k + kSbSlice * sj) * I;
-    gate = p.sh_gate;
-    up = p.sh_up;
-  } else {
-    b -= nshs * tiles;
-    const int s = b / tiles;
-    tile = b - s * tiles;
-    if (s >= g.NS) return;
-    const int u = g.sgrp[s];
-    sj = s - g.spre[u];
-    mask = g.gmask[u];
-    ms = min(kSbSlice, __popc(mask) - kSbSlice * sj);
-    arow0 = (size_t)(g.gpre[u] + kSbSlice * sj) * I;
-    gate = g.ew[g.gent[u]];
-    up = gate + (size_t)I * H;
-  }
-  sb_tokens(g, mask, kSbSlice * sj, ms);
+  const int H = p.H, nkb = H / 128;
   const int n = lane & 15, q = lane >> 4;
   const int rr = min(n, ms - 1);
   // B: load jj of a stage reads weight row 4 jj + q (gate rows 0-7, up rows 8-15 of
@@ -428,7 +394,7 @@ __global__ __launch_bounds__(64) void k_sb_up(SbParams p) {
   // A: load j reads chunk n of token row min(4 j + q, ms - 1) of the slice.
   const uint16_t* pa[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) pa[j] = p.x + (size_t)g.toks[min(4 * j + q, ms - 1)] * H + n * 8;
+  for (int j = 0; j < 2; ++j) pa[j] = p.x + (size_t)tok[j] * H + n * 8;
   u32x4 bq[R][4], aq[R][2];
   auto load = [&](int slot, int st) {
 #pragma unroll
@@ -476,41 +442,36 @@ __global__ __launch_bounds__(64) void k_sb_up(SbParams p) {
       if (r < ms) dst[r * 8] = f32_to_bf16(swiglu_bf16(rbf16(acc[v]), rbf16(upv[v])));
     }
   }
-  if (shared && blockIdx.x < (unsigned)T) {            // the shared expert's gate of token blockIdx.x
-    const int t = blockIdx.x;
-    float a = 0.f;
-    for (int c = lane; c < H / 8; c += 64) a = dot8bb(ld16(p.sh_gate_w + c * 8), ld16(p.x + (size_t)t * H + c * 8), a);
-    a = wave_sum(a);
-    if (lane == 0) p.gs[t] = rbf16(sigmoid_f32(rbf16(a)));
-  }
 }
 
-// Down: one wave per (slice, 32 output columns) (two 16-column MFMA tiles sharing the A
-// fragments); the slice comes from the up kernel's descriptors, so a wave's first weight
-// load issues after one descriptor read.  Last wave of a 64-column tile combines it.
+// The shared expert's gate of token t: bf16(sigmoid(bf16(x_t . w_sg))), one wave.
+__device__ __forceinline__ void sb_shared_gate(const SbParams& p, int t) {
+  const int lane = threadIdx.x & 63, H = p.H;
+  float a = 0.f;
+  for (int c = lane; c < H / 8; c += 64) a = dot8bb(ld16(p.sh_gate_w + c * 8), ld16(p.x + (size_t)t * H + c * 8), a);
+  a = wave_sum(a);
+  if (lane == 0) p.gs[t] = rbf16(sigmoid_f32(rbf16(a)));
+}
+
+// Shared slice sj's up tile `tile` (rows: tokens 8 sj ..), the shared gate of token `gate_t`
+// when gate_t < T.
 template <int R>
-__global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
-  __shared__ u32x4 bt[32 * 17];                       // a stage's 32 weight rows x 16 chunks, rows padded
-  __shared__ u32x4 at[8 * 17];                        // a stage's activations, chunks x rows
-  __shared__ __align__(16) uint16_t dt[16][32];      // the outputs, rows x columns
-  __shared__ SbOrder so;                              // the combine order (for the tile's last wave)
-  const int lane = threadIdx.x;
+__device__ __forceinline__ void sb_shared_up(const SbParams& p, int sj, int tile, int gate_t, u32x4* bt, u32x4* at) {
+  const int T = p.T, I = p.I;
+  const int ms = min(kSbSlice, T - kSbSlice * sj), q = (int)threadIdx.x >> 4;
+  const int tok[2] = {kSbSlice * sj + min(q, ms - 1), kSbSlice * sj + min(4 + q, ms - 1)};
+  sb_up_tile<R>(p, p.sh_gate, p.sh_up, tile, (size_t)(T * p.k + kSbSlice * sj) * I, ms, tok, bt, at);
+  if (gate_t < T) sb_shared_gate(p, gate_t);
+}
+
+// Down work of one (slice, 32 output columns) tile: two 16-column MFMA tiles sharing the A
+// fragments, I / 128 stages (R in flight); d = bf16(acc) to the slice's output rows with
+// 8-byte agent-scope atomic stores.  bt, at, dt: the wave's LDS.
+template <int R>
+__device__ __forceinline__ void sb_down_tile(const SbParams& p, const SbSlice& d, int tile, u32x4* bt, u32x4* at,
+                                             uint16_t (*dt)[32]) {
+  const int lane = threadIdx.x & 63;
   const int H = p.H, I = p.I, nkb = I / 128;
-  const int tiles = H / 32;
-  const int si = blockIdx.x / tiles, tile = blockIdx.x - si * tiles;
-  const int total = (int)p.slices[0].arow;
-  SbOrderRegs ordr;
-  if (si >= total) {
-    // No slice at all: the output is zero (plus the residual).
-    if (total == 0 && si == 0 && (tile & 1) == 0) {
-      ordr.load(p, lane);
-      ordr.store(so, lane);
-      sb_combine(p, so, tile * 32, 64);
-    }
-    return;
-  }
-  const SbSlice d = p.slices[1 + si];
-  ordr.load(p, lane);
   const int ms = d.ms;
   const int n = lane & 15, q = lane >> 4;
   const int rr = min(n, ms - 1);
@@ -561,7 +522,7 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
   uint16_t* obase = d.shared ? p.sh : p.ch;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int r = lane >> 3, c = 4 * (lane & 7) ;           // 8 lanes per row, 32 columns
+    const int r = lane >> 3, c = 4 * (lane & 7);           // 8 lanes per row, 32 columns
     const int rw = r + 8 * h;
     if (rw < ms) {
       const uint64_t word = *reinterpret_cast<const uint64_t*>(&dt[rw][c]);
@@ -569,6 +530,125 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+
+// The shared slice sj as a down slice.
+__device__ __forceinline__ SbSlice sb_shared_slice(const SbParams& p, int sj) {
+  SbSlice d;
+  d.w = p.sh_down;
+  d.ms = (uint8_t)min(kSbSlice, p.T - kSbSlice * sj);
+  d.orow = (uint16_t)(kSbSlice * sj);
+  d.arow = (uint32_t)((p.T * p.k + kSbSlice * sj) * p.I);
+  d.shared = 1;
+  return d;
+}
+
+// Up: one wave per (slice, 8 activation columns).  Block `duty` (the first block after the
+// shared down tiles) also writes the combine order and the down kernel's slice descriptors.
+// Without sh_pre the shared slices come first, and blocks 0 .. T-1 (shared slice 0) compute
+// the shared gate; with sh_pre (SHD) the first blocks are the shared expert's down tiles (its
+// activations came from the router launch), one per (shared slice, 32 output columns).
+template <int R, bool SHD>
+__global__ __launch_bounds__(64, 3) void k_sb_up(SbParams p) {
+  // The shared down tiles need no groups: the two uses share the block's LDS.
+  struct UpLds {
+    SbGroups g;
+    u32x4 bt[16 * 17];                                // a stage's 16 weight rows x 16 chunks, rows padded
+    u32x4 at[8 * 17];                                 // a stage's token rows x 16 chunks, rows padded
+  };
+  struct DnLds {
+    u32x4 bt[32 * 17];
+    u32x4 at[8 * 17];
+    __align__(16) uint16_t dt[16][32];
+  };
+  __shared__ union {
+    UpLds up;
+    DnLds dn;
+  } sm;
+  const int T = p.T, H = p.H, I = p.I;
+  const int tiles = I / 8;
+  const int nshs = p.sh_gate ? (T + kSbSlice - 1) / kSbSlice : 0;
+  const int nshd = SHD ? nshs * (H / 32) : 0;
+  int b = blockIdx.x;
+  if constexpr (SHD) {
+    if (b < nshd) {
+      const int sj = b / (H / 32);
+      sb_down_tile<2>(p, sb_shared_slice(p, sj), b - sj * (H / 32), sm.dn.bt, sm.dn.at, sm.dn.dt);
+      return;
+    }
+  }
+  SbGroups& g = sm.up.g;
+  const bool duty = b == nshd;
+  b -= nshd;
+  const int nshu = SHD ? 0 : nshs * tiles;
+  const bool shared_up = b < nshu;
+  if (duty || !shared_up) {                           // shared up tiles need no groups either
+    sb_groups(p, g, duty);
+    if (duty) {
+      sb_order(p, g);
+      sb_slices(p, g);
+    }
+  }
+  // One tile body for both kinds (two inlined copies cost registers).
+  const uint16_t *gate, *up;
+  int tile, ms, sj;
+  uint32_t mask;
+  size_t arow0;
+  if (shared_up) {
+    sj = b / tiles;
+    tile = b - sj * tiles;
+    mask = (1u << T) - 1u;
+    ms = min(kSbSlice, T - kSbSlice * sj);
+    arow0 = (size_t)(T * p.k + kSbSlice * sj) * I;
+    gate = p.sh_gate;
+    up = p.sh_up;
+  } else {
+    b -= nshu;
+    const int s = b / tiles;
+    tile = b - s * tiles;
+    if (s >= g.NS) return;
+    const int u = g.sgrp[s];
+    sj = s - g.spre[u];
+    mask = g.gmask[u];
+    ms = min(kSbSlice, __popc(mask) - kSbSlice * sj);
+    arow0 = (size_t)(g.gpre[u] + kSbSlice * sj) * I;
+    gate = g.ew[g.gent[u]];
+    up = gate + (size_t)I * H;
+  }
+  sb_tokens(g, mask, kSbSlice * sj, ms);
+  const int q = (int)threadIdx.x >> 4;
+  const int tok[2] = {g.toks[min(q, ms - 1)], g.toks[min(4 + q, ms - 1)]};
+  sb_up_tile<R>(p, gate, up, tile, arow0, ms, tok, sm.up.bt, sm.up.at);
+  if (shared_up && blockIdx.x < (unsigned)T) sb_shared_gate(p, blockIdx.x);   // the shared gate of token blockIdx.x
+}
+
+// Down: one wave per (slice, 32 output columns); the slice comes from the up kernel's
+// descriptors, so a wave's first weight load issues after one descriptor read.  The last wave
+// of a 64-column tile combines it.
+template <int R>
+__global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
+  __shared__ u32x4 bt[32 * 17];                       // a stage's 32 weight rows x 16 chunks, rows padded
+  __shared__ u32x4 at[8 * 17];                        // a stage's activations, chunks x rows
+  __shared__ __align__(16) uint16_t dt[16][32];      // the outputs, rows x columns
+  __shared__ SbOrder so;                              // the combine order (for the tile's last wave)
+  const int lane = threadIdx.x;
+  const int H = p.H;
+  const int tiles = H / 32;
+  const int si = blockIdx.x / tiles, tile = blockIdx.x - si * tiles;
+  const int total = (int)p.slices[0].arow;
+  SbOrderRegs ordr;
+  if (si >= total) {
+    // No slice at all: the output is the shared expert's (or zero), plus the residual.
+    if (total == 0 && si == 0 && (tile & 1) == 0) {
+      ordr.load(p, lane);
+      ordr.store(so, lane);
+      sb_combine(p, so, tile * 32, 64);
+    }
+    return;
+  }
+  const SbSlice d = p.slices[1 + si];
+  ordr.load(p, lane);
+  sb_down_tile<R>(p, d, tile, bt, at, dt);
   // Arrival on the 64-column combine tile once the stores have completed; the last of its
   // 2 x (slices) waves combines it and re-zeroes the counter.
   sb_stores_done();
@@ -583,17 +663,28 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
   if (lane == 0) __hip_atomic_store(p.cnt + ct * kLine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Router logits and per-token top-k.  Block (t, y) of kSbRouterWaves waves: wave w computes
-// logits 4 (y kSbRouterWaves + w) .. + 3 of token t and stores them with agent-scope atomic
-// stores; the token's last block selects.  One-wave blocks spread the router weight's read over
-// E / 4 CUs per token (4-wave blocks, a quarter as many CUs: T=2 63.4 against 62.7 us per layer).
-template <int MAXC, int MAXEPL>
+// Router logits and per-token top-k.  Block (t, y < nb) computes logits 4 y .. 4 y + 3 of token
+// t and stores them with agent-scope atomic stores; the token's last block selects.  One-wave
+// blocks spread the router weight's read over E / 4 CUs per token (4-wave blocks, a quarter as
+// many CUs: T=2 63.4 against 62.7 us per layer).  Blocks (t, y >= nb), when sp.sh_pre, run the
+// shared expert's up tiles and gate, which need no routing: (y - nb) T + t indexes the shared
+// slices' tiles (R stages in flight), and tile indexes below T compute token j's gate.
+template <int MAXC, int MAXEPL, int R>
 __global__ __launch_bounds__(64 * kSbRouterWaves) void k_sb_router(const uint16_t* __restrict__ x,
                                                                    const uint16_t* __restrict__ wg, int H, int E,
-                                                                   int k, float* logits, uint32_t* cnt, TopkOut o) {
+                                                                   int k, int nb, float* logits, uint32_t* cnt,
+                                                                   TopkOut o, SbParams sp) {
+  static_assert(kSbRouterWaves == 1, "the shared up tiles are one-wave blocks");
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int t = blockIdx.x;
   __shared__ int last;
+  if ((int)blockIdx.y >= nb) {
+    __shared__ u32x4 bt[16 * 17], at[8 * 17];
+    const int j = ((int)blockIdx.y - nb) * (int)gridDim.x + t, tiles = sp.I / 8;
+    const int sj = j / tiles;
+    if (sj < (sp.T + kSbSlice - 1) / kSbSlice) sb_shared_up<R>(sp, sj, j - sj * tiles, j, bt, at);
+    return;
+  }
   XFrag<MAXC> xf;
   load_xfrag<MAXC>(xf, x + (size_t)t * H, H, lane);
   const int e0 = ((int)blockIdx.y * kSbRouterWaves + wid) * 4;
@@ -613,8 +704,7 @@ __global__ __launch_bounds__(64 * kSbRouterWaves) void k_sb_router(const uint16_
   sb_stores_done();
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(cnt + t * kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           gridDim.y - 1u;
+    last = __hip_atomic_fetch_add(cnt + t * kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)nb - 1u;
   __syncthreads();
   if (!last) return;
   if (wid == 0) {
@@ -641,27 +731,43 @@ bool sb_supported(int T, int H, int I, int Is, int k, int q4) {
 }
 
 static void sb_launch_up(const SbParams& p, int R, dim3 grid, hipStream_t s) {
+  const bool shd = p.sh_pre != 0;   // only with R = 4 or 5 (sb_shared_pre)
   switch (R) {
-    case 5: hipLaunchKernelGGL((k_sb_up<5>), grid, dim3(64), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((k_sb_up<4>), grid, dim3(64), 0, s, p); break;
-    case 3: hipLaunchKernelGGL((k_sb_up<3>), grid, dim3(64), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((k_sb_up<2>), grid, dim3(64), 0, s, p); break;
-    default: hipLaunchKernelGGL((k_sb_up<1>), grid, dim3(64), 0, s, p); break;
+    case 5:
+      if (shd) hipLaunchKernelGGL((k_sb_up<5, true>), grid, dim3(64), 0, s, p);
+      else hipLaunchKernelGGL((k_sb_up<5, false>), grid, dim3(64), 0, s, p);
+      break;
+    case 4:
+      if (shd) hipLaunchKernelGGL((k_sb_up<4, true>), grid, dim3(64), 0, s, p);
+      else hipLaunchKernelGGL((k_sb_up<4, false>), grid, dim3(64), 0, s, p);
+      break;
+    case 3: hipLaunchKernelGGL((k_sb_up<3, false>), grid, dim3(64), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((k_sb_up<2, false>), grid, dim3(64), 0, s, p); break;
+    default: hipLaunchKernelGGL((k_sb_up<1, false>), grid, dim3(64), 0, s, p); break;
   }
 }
 
-// Shapes must pass sb_supported; the workspace is ws_layout(T, H, E, I, k, Is).
-int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
-              const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
-              const uint16_t* sh_down, const uint16_t* sh_gate_w, int H, int E, int I, int k, int Is,
-              uint16_t* out, void* ws, hipStream_t s, const uint16_t* resid, uint32_t* err) {
-  const bool has_sh = sh_gate != nullptr;
-  if (!has_sh) Is = 0;
-  if (!sb_supported(T, H, I, Is, k, 0)) return TMOE_ERR_SHAPE;
+// Whether the router launch can take the shared expert's gate/up (and the up launch its down):
+// a shared expert, up tiles of 4 or 5 stages in flight, down tiles of 2, E <= 256.
+static bool sb_shared_pre(bool has_sh, int H, int E, int I) {
+  const int r = sb_ring(H / 128, 5);
+  return has_sh && (r == 4 || r == 5) && sb_ring(I / 128, 2) == 2 && E <= 256;
+}
+// Token counts that take it.  Full-size layer (H=2560, E=256, I=1024, k=8, 8 rotating layers,
+// same-run A/B, three rounds): T=2 62.6-62.9 -> 61.1-61.4 us (router 7.6 -> 8.5, up 31.7 -> 30.5,
+// down 23.8 -> 22.4); T=4 95.5 -> 97.0, T=8 156.4 -> 159.5, T=16 260 -> 263-266: with more
+// tokens the shared slice is a smaller part of the up and down launches, and the router launch
+// then waits for its shared tiles (each wave streams 80 KB in four ring lengths, ~8 us; a
+// delay before them made T=2 slower still: 62.1 / 62.9 / 64.6 us for ~1 / 2 / 4 us).
+static bool sb_shared_pre_tokens(int T) { return T == 2; }
+
+static SbParams sb_params(const uint16_t* x, int T, const uint16_t* sh_gate, const uint16_t* sh_up,
+                          const uint16_t* sh_down, const uint16_t* sh_gate_w, int H, int E, int I, int k, int Is,
+                          void* ws) {
   const Ws L = ws_layout(T, H, E, I, k, Is);
   SbParams p{};
-  p.x = x; p.ids32 = ids32; p.ids64 = ids64; p.wf = wf; p.wb = wb; p.table = table;
-  p.sh_gate = sh_gate; p.sh_up = sh_up; p.sh_down = sh_down; p.sh_gate_w = sh_gate_w; p.resid = resid;
+  p.x = x;
+  p.sh_gate = sh_gate; p.sh_up = sh_up; p.sh_down = sh_down; p.sh_gate_w = sh_gate_w;
   p.T = T; p.H = H; p.E = E; p.I = I; p.k = k;
   p.act = ws_ptr<uint16_t>(ws, L.act);
   p.ch = ws_ptr<uint16_t>(ws, L.ch);
@@ -672,15 +778,37 @@ int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids
   p.ord_n = p.ord_row + 2 * kSbMaxEntries;
   p.cnt = ws_ptr<uint32_t>(ws, L.sync) + kLnSbTile * kLine;
   p.slices = reinterpret_cast<SbSlice*>(p.ord_n + kSbMaxTokens);
-  p.err = err ? err : ws_ptr<uint32_t>(ws, L.status) + kStatusError;
+  p.err = ws_ptr<uint32_t>(ws, L.status) + kStatusError;
+  return p;
+}
+
+// Shapes must pass sb_supported; the workspace is ws_layout(T, H, E, I, k, Is).  sh_pre: the
+// router launch on this stream just ran the shared expert's gate/up and gate (sb_router_launch
+// reported it).
+int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids64, const float* wf,
+              const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
+              const uint16_t* sh_down, const uint16_t* sh_gate_w, int H, int E, int I, int k, int Is,
+              uint16_t* out, void* ws, hipStream_t s, const uint16_t* resid, uint32_t* err, int sh_pre) {
+  const bool has_sh = sh_gate != nullptr;
+  if (!has_sh) Is = 0;
+  if (!sb_supported(T, H, I, Is, k, 0)) return TMOE_ERR_SHAPE;
+  if (sh_pre && !sb_shared_pre(has_sh, H, E, I)) return TMOE_ERR_SHAPE;
+  SbParams p = sb_params(x, T, sh_gate, sh_up, sh_down, sh_gate_w, H, E, I, k, Is, ws);
+  p.ids32 = ids32; p.ids64 = ids64; p.wf = wf; p.wb = wb; p.table = table;
+  p.resid = resid;
+  if (err) p.err = err;
   p.out = out;
+  p.sh_pre = sh_pre ? 1 : 0;
   // Slices: each group is ceil(m / 8) slices, at most T*k in all (min(E, T*k) when T <= 8).
   const int groups = E < T * k ? E : T * k;
   const int slices = T <= kSbSlice ? groups : (T * k < 2 * groups ? T * k : 2 * groups);
   const int nshs = has_sh ? (T + kSbSlice - 1) / kSbSlice : 0;
-  sb_launch_up(p, sb_ring(H / 128, 5), dim3((unsigned)((nshs + slices) * (I / 8))), s);
+  // Up launch: the shared slices' up tiles, or with sh_pre their down tiles, then the routed
+  // slices' up tiles.
+  const int up_blocks = (sh_pre ? nshs * (H / 32) : nshs * (I / 8)) + slices * (I / 8);
+  sb_launch_up(p, sb_ring(H / 128, 5), dim3((unsigned)up_blocks), s);
   {
-    const dim3 grid((unsigned)((nshs + slices) * (H / 32)));
+    const dim3 grid((unsigned)(((sh_pre ? 0 : nshs) + slices) * (H / 32)));
     // Two stages of 32 rows in flight (deeper rings measured no faster and cost a wave slot).
     if (sb_ring(I / 128, 2) == 2) hipLaunchKernelGGL((k_sb_down<2>), grid, dim3(64), 0, s, p);
     else hipLaunchKernelGGL((k_sb_down<1>), grid, dim3(64), 0, s, p);
@@ -689,9 +817,14 @@ int sb_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t* ids
 }
 
 // Router logits and top-k for 2 <= T <= kSbMaxTokens tokens in one launch: ids32 / wf to the
-// workspace, ids64 / wb to the caller (optional), heat counters (optional).
+// workspace, ids64 / wb to the caller (optional), heat counters (optional).  With a shared
+// expert (and shapes sb_shared_pre takes) the same launch runs the shared expert's gate/up and
+// gate, and *sh_pre is set for sb_launch; the shared weights are then read while the routing
+// resolves.
 int sb_router_launch(const uint16_t* x, const uint16_t* wg, int T, int H, int E, int I, int k, int Is,
-                     int64_t* ids64, uint16_t* wb, uint32_t* heat, void* ws, hipStream_t s) {
+                     const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_gate_w, int64_t* ids64,
+                     uint16_t* wb, uint32_t* heat, void* ws, hipStream_t s, int* sh_pre) {
+  *sh_pre = 0;
   if (T < 1 || T > kSbMaxTokens || H % 8 || H > kMaxDim || E > kMaxExperts) return TMOE_ERR_SHAPE;
   const Ws L = ws_layout(T, H, E, I, k, Is);
   TopkOut o{};
@@ -702,12 +835,18 @@ int sb_router_launch(const uint16_t* x, const uint16_t* wg, int T, int H, int E,
   o.heat = heat;
   float* logits = ws_ptr<float>(ws, L.logits);
   uint32_t* cnt = ws_ptr<uint32_t>(ws, L.sync) + kLnSbRouter * kLine;
-  const dim3 g(T, (E + 4 * kSbRouterWaves - 1) / (4 * kSbRouterWaves)), b(64 * kSbRouterWaves);
+  const bool pre = sb_shared_pre_tokens(T) && sb_supported(T, H, I, Is, k, 0) &&
+                   sb_shared_pre(sh_gate != nullptr, H, E, I);
+  SbParams sp = sb_params(x, T, sh_gate, sh_up, nullptr, sh_gate_w, H, E, I, k, Is, ws);
+  const int nb = (E + 4 * kSbRouterWaves - 1) / (4 * kSbRouterWaves);
+  const int shared_tiles = pre ? (T + kSbSlice - 1) / kSbSlice * (I / 8) : 0;
+  const dim3 g(T, nb + (shared_tiles + T - 1) / T), b(64 * kSbRouterWaves);
   const int nc = (H + 511) / 512;
-  const bool small_e = E <= 256;
-#define TMOE_SB_ROUTER(MAXC)                                                                                  \
-  if (small_e) hipLaunchKernelGGL((k_sb_router<MAXC, 4>), g, b, 0, s, x, wg, H, E, k, logits, cnt, o);     \
-  else hipLaunchKernelGGL((k_sb_router<MAXC, 16>), g, b, 0, s, x, wg, H, E, k, logits, cnt, o);
+  const bool r5 = sb_ring(H / 128, 5) == 5;
+#define TMOE_SB_ROUTER(MAXC)                                                                                   \
+  if (E > 256) hipLaunchKernelGGL((k_sb_router<MAXC, 16, 4>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp); \
+  else if (r5) hipLaunchKernelGGL((k_sb_router<MAXC, 4, 5>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp);  \
+  else hipLaunchKernelGGL((k_sb_router<MAXC, 4, 4>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp);
   switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
     case 2: TMOE_SB_ROUTER(2) break;
     case 4: TMOE_SB_ROUTER(4) break;
@@ -715,7 +854,9 @@ int sb_router_launch(const uint16_t* x, const uint16_t* wg, int T, int H, int E,
     default: TMOE_SB_ROUTER(8) break;
   }
 #undef TMOE_SB_ROUTER
-  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+  if (hipGetLastError() != hipSuccess) return TMOE_ERR_HIP;
+  *sh_pre = pre ? 1 : 0;
+  return TMOE_OK;
 }
 
 }  // namespace tmoe

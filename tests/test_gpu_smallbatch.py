@@ -57,10 +57,12 @@ def test_small_batch_block_full_size(gpu, T):
     _block_case(FULL, T, 400 + T, gpu)
 
 
-@pytest.mark.parametrize("shape,T,seed", [(MID, 6, 77), (FULL, 2, 78), (FULL, 16, 79)])
+@pytest.mark.parametrize("shape,T,seed", [(MID, 2, 76), (MID, 6, 77), (FULL, 2, 78), (FULL, 16, 79)])
 def test_small_batch_router_weights_path(gpu, shape, T, seed):
     """Router logits computed on the device (fp32 GEMV) before the small-batch experts, at the
-    mid shape and at the full-size layer (H=2560, E=256) for the smallest and largest T."""
+    mid shape and at the full-size layer (H=2560, E=256) for the smallest and largest T.  At
+    T = 2 the router launch also runs the shared expert's gate/up and gate, and the up launch
+    its down (4-stage up tiles at H = 1024, 5-stage at H = 2560)."""
     layer = seeded.make_layer(shape, seed, device=gpu)
     ws = Workspace(shape, gpu, tokens=T)
     table = tm.expert_table(layer.gate_up, layer.down)
