@@ -10,8 +10,10 @@
 //              entries in ascending expert id (ties in slot order), each bf16(d * w) added
 //              with a bf16 rounding, then the shared expert bf16(d_s * gate)
 //                                        fused_int4.py:243-244, modeling_qwen3_5_moe.py:796
-//   k_sb_router  (block entry) fp32 router logits, T x E/16 blocks; the last block of each
-//              token selects its top-k (modeling_qwen3_5_moe.py:768-776).
+//   k_sb_router  (block entry) fp32 router logits, T x E/4 one-wave blocks; the last block of
+//              each token selects its top-k (modeling_qwen3_5_moe.py:768-776).  At T = 2 it also
+//              runs the shared expert's gate/up and gate (they need no routing), and the up
+//              launch (k_sb_up_shd) then runs the shared expert's down beside the routed up tiles.
 //
 // Streaming.  The slice's token rows are the MFMA A operand (v_mfma_f32_16x16x32_bf16; rows
 // past the slice repeat a real row and are never written), the weight rows the B operand.
@@ -371,34 +373,38 @@ __device__ void sb_combine(const SbParams& p, const SbOrder& o, int c0, int ncol
   }
 }
 
-// Up work of one (slice, 8 activation columns) tile: 8 gate and 8 up weight rows over K = H
+// Up work of one (slice, NC activation columns) tile: NC gate and NC up weight rows over K = H
 // (H / 128 stages, R in flight), act = bf16(bf16(silu(bf16 g)) * bf16 u) for the slice's ms
 // token rows into the activations at arow0.  The lane's A rows: tok[j] = the token of slice
-// row min(4 j + lane / 16, ms - 1).  bt, at: the wave's LDS.
-template <int R>
+// row min(4 j + lane / 16, ms - 1).  bt, at: the wave's LDS.  NC = 8 fills the MFMA's 16
+// columns; NC = 4 (rows 8-15 of B repeat rows 0-7) halves a tile's bytes, for tiles that must
+// finish in fewer ring lengths.
+template <int R, int NC = 8>
 __device__ __forceinline__ void sb_up_tile(const SbParams& p, const uint16_t* gate, const uint16_t* up, int tile,
                                            size_t arow0, int ms, const int (&tok)[2], u32x4* bt, u32x4* at) {
+  static_assert(NC == 8 || NC == 4, "8 or 4 activation columns per tile");
+  constexpr int NB = NC / 2;                          // weight loads per stage (4 rows each)
   const int lane = threadIdx.x;
   const int H = p.H, nkb = H / 128;
   const int n = lane & 15, q = lane >> 4;
   const int rr = min(n, ms - 1);
-  // B: load jj of a stage reads weight row 4 jj + q (gate rows 0-7, up rows 8-15 of
-  // activation columns 8 tile ..); lane (c, q) takes 16-byte chunk c of the stage's 256
+  // B: load jj of a stage reads weight row 4 jj + q (gate rows 0 .. NC-1, up rows NC .. 2NC-1
+  // of activation columns NC tile ..); lane (c, q) takes 16-byte chunk c of the stage's 256
   // bytes of that row: two whole cache lines per row per load.
-  const uint16_t* pb[4];
+  const uint16_t* pb[NB];
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
+  for (int jj = 0; jj < NB; ++jj) {
     const int rw = 4 * jj + q;
-    pb[jj] = (rw < 8 ? gate : up) + (size_t)(tile * 8 + (rw & 7)) * H + n * 8;
+    pb[jj] = (rw < NC ? gate : up) + (size_t)(tile * NC + rw % NC) * H + n * 8;
   }
   // A: load j reads chunk n of token row min(4 j + q, ms - 1) of the slice.
   const uint16_t* pa[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) pa[j] = p.x + (size_t)tok[j] * H + n * 8;
-  u32x4 bq[R][4], aq[R][2];
+  u32x4 bq[R][NB], aq[R][2];
   auto load = [&](int slot, int st) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) bq[slot][jj] = ld_stream(pb[jj] + st * 128);
+    for (int jj = 0; jj < NB; ++jj) bq[slot][jj] = ld_stream(pb[jj] + st * 128);
 #pragma unroll
     for (int j = 0; j < 2; ++j) aq[slot][j] = ld16(pa[j] + st * 128);
   };
@@ -407,13 +413,13 @@ __device__ __forceinline__ void sb_up_tile(const SbParams& p, const uint16_t* ga
   // of weight row r (B) and of token row rr (A).
   auto mult = [&](int slot) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) bt[(4 * jj + q) * 17 + n] = bq[slot][jj];
+    for (int jj = 0; jj < NB; ++jj) bt[(4 * jj + q) * 17 + n] = bq[slot][jj];
 #pragma unroll
     for (int j = 0; j < 2; ++j) at[(4 * j + q) * 17 + n] = aq[slot][j];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sb_frag(at[rr * 17 + 4 * i + q]), sb_frag(bt[n * 17 + 4 * i + q]),
-                                                    acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sb_frag(at[rr * 17 + 4 * i + q]),
+                                                    sb_frag(bt[(n % (2 * NC)) * 17 + 4 * i + q]), acc, 0, 0, 0);
     // One stage's fragments live at a time (the scheduler would otherwise hoist the next
     // stage's LDS reads and cost a wave slot per SIMD).
     __builtin_amdgcn_sched_barrier(0);
@@ -429,13 +435,15 @@ __device__ __forceinline__ void sb_up_tile(const SbParams& p, const uint16_t* ga
   }
 #pragma unroll
   for (int st = 0; st < R; ++st) mult(st);
-  // C: lane (n, q) holds column n (0-7 gate, 8-15 up of activation column 8 tile + n % 8) of
-  // rows 4q .. 4q + 3.
+  // C: lane (n, q) holds column n (0 .. NC-1 gate, NC .. 2NC-1 up of activation column
+  // NC tile + n % NC) of rows 4q .. 4q + 3; activation column c of row r lives at element
+  // ((c / 8) ms + r) 8 + c % 8.
   float upv[4];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) upv[v] = __shfl(acc[v], lane + 8);
-  if (n < 8) {
-    uint16_t* dst = p.act + arow0 + (size_t)tile * ms * 8 + n;
+  for (int v = 0; v < 4; ++v) upv[v] = __shfl(acc[v], lane + NC);
+  if (n < NC) {
+    const int c = tile * NC + n;
+    uint16_t* dst = p.act + arow0 + (size_t)(c >> 3) * ms * 8 + (c & 7);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int r = 4 * q + v;
@@ -453,14 +461,14 @@ __device__ __forceinline__ void sb_shared_gate(const SbParams& p, int t) {
   if (lane == 0) p.gs[t] = rbf16(sigmoid_f32(rbf16(a)));
 }
 
-// Shared slice sj's up tile `tile` (rows: tokens 8 sj ..), the shared gate of token `gate_t`
-// when gate_t < T.
-template <int R>
+// Shared slice sj's up tile `tile` of NC columns (rows: tokens 8 sj ..), the shared gate of
+// token `gate_t` when gate_t < T.
+template <int R, int NC>
 __device__ __forceinline__ void sb_shared_up(const SbParams& p, int sj, int tile, int gate_t, u32x4* bt, u32x4* at) {
   const int T = p.T, I = p.I;
   const int ms = min(kSbSlice, T - kSbSlice * sj), q = (int)threadIdx.x >> 4;
   const int tok[2] = {kSbSlice * sj + min(q, ms - 1), kSbSlice * sj + min(4 + q, ms - 1)};
-  sb_up_tile<R>(p, p.sh_gate, p.sh_up, tile, (size_t)(T * p.k + kSbSlice * sj) * I, ms, tok, bt, at);
+  sb_up_tile<R, NC>(p, p.sh_gate, p.sh_up, tile, (size_t)(T * p.k + kSbSlice * sj) * I, ms, tok, bt, at);
   if (gate_t < T) sb_shared_gate(p, gate_t);
 }
 
@@ -543,13 +551,129 @@ __device__ __forceinline__ SbSlice sb_shared_slice(const SbParams& p, int sj) {
   return d;
 }
 
-// Up: one wave per (slice, 8 activation columns).  Block `duty` (the first block after the
-// shared down tiles) also writes the combine order and the down kernel's slice descriptors.
-// Without sh_pre the shared slices come first, and blocks 0 .. T-1 (shared slice 0) compute
-// the shared gate; with sh_pre (SHD) the first blocks are the shared expert's down tiles (its
-// activations came from the router launch), one per (shared slice, 32 output columns).
-template <int R, bool SHD>
-__global__ __launch_bounds__(64, 3) void k_sb_up(SbParams p) {
+// Up: one wave per (slice, 8 activation columns) = 8 gate and 8 up weight rows over K = H
+// (128 nkb columns, R stages in flight); block 0 also writes the combine order and the down
+// kernel's slice descriptors; blocks 0 .. T-1 (shared slice 0) compute the shared gate.
+template <int R>
+__global__ __launch_bounds__(64) void k_sb_up(SbParams p) {
+  __shared__ SbGroups g;
+  __shared__ u32x4 bt[16 * 17];                       // a stage's 16 weight rows x 16 chunks, rows padded
+  __shared__ u32x4 at[8 * 17];                        // a stage's token rows x 16 chunks, rows padded
+  sb_groups(p, g, blockIdx.x == 0);
+  if (blockIdx.x == 0) {
+    sb_order(p, g);
+    sb_slices(p, g);
+  }
+  const int lane = threadIdx.x;
+  const int T = p.T, H = p.H, I = p.I;
+  const int tiles = I / 8;
+  const int nshs = p.sh_gate ? (T + kSbSlice - 1) / kSbSlice : 0;
+  const int nkb = H / 128;
+  int b = blockIdx.x, tile, sj, ms;
+  uint32_t mask;
+  size_t arow0;
+  const uint16_t *gate, *up;
+  const bool shared = b < nshs * tiles;
+  if (shared) {
+    sj = b / tiles;
+    tile = b - sj * tiles;
+    mask = (1u << T) - 1u;
+    ms = min(kSbSlice, T - kSbSlice * sj);
+    arow0 = (size_t)(T * p.k + kSbSlice * sj) * I;
+    gate = p.sh_gate;
+    up = p.sh_up;
+  } else {
+    b -= nshs * tiles;
+    const int s = b / tiles;
+    tile = b - s * tiles;
+    if (s >= g.NS) return;
+    const int u = g.sgrp[s];
+    sj = s - g.spre[u];
+    mask = g.gmask[u];
+    ms = min(kSbSlice, __popc(mask) - kSbSlice * sj);
+    arow0 = (size_t)(g.gpre[u] + kSbSlice * sj) * I;
+    gate = g.ew[g.gent[u]];
+    up = gate + (size_t)I * H;
+  }
+  sb_tokens(g, mask, kSbSlice * sj, ms);
+  const int n = lane & 15, q = lane >> 4;
+  const int rr = min(n, ms - 1);
+  // B: load jj of a stage reads weight row 4 jj + q (gate rows 0-7, up rows 8-15 of
+  // activation columns 8 tile ..); lane (c, q) takes 16-byte chunk c of the stage's 256
+  // bytes of that row: two whole cache lines per row per load.
+  const uint16_t* pb[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int rw = 4 * jj + q;
+    pb[jj] = (rw < 8 ? gate : up) + (size_t)(tile * 8 + (rw & 7)) * H + n * 8;
+  }
+  // A: load j reads chunk n of token row min(4 j + q, ms - 1) of the slice.
+  const uint16_t* pa[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) pa[j] = p.x + (size_t)g.toks[min(4 * j + q, ms - 1)] * H + n * 8;
+  u32x4 bq[R][4], aq[R][2];
+  auto load = [&](int slot, int st) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) bq[slot][jj] = ld_stream(pb[jj] + st * 128);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) aq[slot][j] = ld16(pa[j] + st * 128);
+  };
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // Through LDS into MFMA fragments: lane (r, q) of MFMA i takes columns 128 s + 32 i + 8 q
+  // of weight row r (B) and of token row rr (A).
+  auto mult = [&](int slot) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) bt[(4 * jj + q) * 17 + n] = bq[slot][jj];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) at[(4 * j + q) * 17 + n] = aq[slot][j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sb_frag(at[rr * 17 + 4 * i + q]), sb_frag(bt[n * 17 + 4 * i + q]),
+                                                    acc, 0, 0, 0);
+    // One stage's fragments live at a time (the scheduler would otherwise hoist the next
+    // stage's LDS reads and cost a wave slot per SIMD).
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int st = 0; st < R; ++st) load(st, st);
+  for (int kb0 = 0; kb0 + R < nkb; kb0 += R) {
+#pragma unroll
+    for (int st = 0; st < R; ++st) {
+      mult(st);
+      load(st, kb0 + st + R);
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < R; ++st) mult(st);
+  // C: lane (n, q) holds column n (0-7 gate, 8-15 up of activation column 8 tile + n % 8) of
+  // rows 4q .. 4q + 3.
+  float upv[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) upv[v] = __shfl(acc[v], lane + 8);
+  if (n < 8) {
+    uint16_t* dst = p.act + arow0 + (size_t)tile * ms * 8 + n;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * q + v;
+      if (r < ms) dst[r * 8] = f32_to_bf16(swiglu_bf16(rbf16(acc[v]), rbf16(upv[v])));
+    }
+  }
+  if (shared && blockIdx.x < (unsigned)T) {            // the shared expert's gate of token blockIdx.x
+    const int t = blockIdx.x;
+    float a = 0.f;
+    for (int c = lane; c < H / 8; c += 64) a = dot8bb(ld16(p.sh_gate_w + c * 8), ld16(p.x + (size_t)t * H + c * 8), a);
+    a = wave_sum(a);
+    if (lane == 0) p.gs[t] = rbf16(sigmoid_f32(rbf16(a)));
+  }
+}
+
+// Up launch with sh_pre: the first blocks are the shared expert's down tiles (its activations
+// came from the router launch), one per (shared slice, 32 output columns); then one wave per
+// routed (slice, 8 activation columns) as in k_sb_up, block `duty` (the first routed one)
+// writing the combine order and the down kernel's slice descriptors.  Three waves per SIMD
+// (168 registers) keep a T=2 grid resident.
+template <int R>
+__global__ __launch_bounds__(64, 3) void k_sb_up_shd(SbParams p) {
   // The shared down tiles need no groups: the two uses share the block's LDS.
   struct UpLds {
     SbGroups g;
@@ -568,58 +692,33 @@ __global__ __launch_bounds__(64, 3) void k_sb_up(SbParams p) {
   const int T = p.T, H = p.H, I = p.I;
   const int tiles = I / 8;
   const int nshs = p.sh_gate ? (T + kSbSlice - 1) / kSbSlice : 0;
-  const int nshd = SHD ? nshs * (H / 32) : 0;
+  const int nshd = nshs * (H / 32);
   int b = blockIdx.x;
-  if constexpr (SHD) {
-    if (b < nshd) {
-      const int sj = b / (H / 32);
-      sb_down_tile<2>(p, sb_shared_slice(p, sj), b - sj * (H / 32), sm.dn.bt, sm.dn.at, sm.dn.dt);
-      return;
-    }
+  if (b < nshd) {
+    const int sj = b / (H / 32);
+    sb_down_tile<2>(p, sb_shared_slice(p, sj), b - sj * (H / 32), sm.dn.bt, sm.dn.at, sm.dn.dt);
+    return;
   }
   SbGroups& g = sm.up.g;
   const bool duty = b == nshd;
   b -= nshd;
-  const int nshu = SHD ? 0 : nshs * tiles;
-  const bool shared_up = b < nshu;
-  if (duty || !shared_up) {                           // shared up tiles need no groups either
-    sb_groups(p, g, duty);
-    if (duty) {
-      sb_order(p, g);
-      sb_slices(p, g);
-    }
+  sb_groups(p, g, duty);
+  if (duty) {
+    sb_order(p, g);
+    sb_slices(p, g);
   }
-  // One tile body for both kinds (two inlined copies cost registers).
-  const uint16_t *gate, *up;
-  int tile, ms, sj;
-  uint32_t mask;
-  size_t arow0;
-  if (shared_up) {
-    sj = b / tiles;
-    tile = b - sj * tiles;
-    mask = (1u << T) - 1u;
-    ms = min(kSbSlice, T - kSbSlice * sj);
-    arow0 = (size_t)(T * p.k + kSbSlice * sj) * I;
-    gate = p.sh_gate;
-    up = p.sh_up;
-  } else {
-    b -= nshu;
-    const int s = b / tiles;
-    tile = b - s * tiles;
-    if (s >= g.NS) return;
-    const int u = g.sgrp[s];
-    sj = s - g.spre[u];
-    mask = g.gmask[u];
-    ms = min(kSbSlice, __popc(mask) - kSbSlice * sj);
-    arow0 = (size_t)(g.gpre[u] + kSbSlice * sj) * I;
-    gate = g.ew[g.gent[u]];
-    up = gate + (size_t)I * H;
-  }
+  const int s = b / tiles, tile = b - s * tiles;
+  if (s >= g.NS) return;
+  const int u = g.sgrp[s];
+  const int sj = s - g.spre[u];
+  const uint32_t mask = g.gmask[u];
+  const int ms = min(kSbSlice, __popc(mask) - kSbSlice * sj);
+  const uint16_t* gate = g.ew[g.gent[u]];
   sb_tokens(g, mask, kSbSlice * sj, ms);
   const int q = (int)threadIdx.x >> 4;
   const int tok[2] = {g.toks[min(q, ms - 1)], g.toks[min(4 + q, ms - 1)]};
-  sb_up_tile<R>(p, gate, up, tile, arow0, ms, tok, sm.up.bt, sm.up.at);
-  if (shared_up && blockIdx.x < (unsigned)T) sb_shared_gate(p, blockIdx.x);   // the shared gate of token blockIdx.x
+  sb_up_tile<R>(p, gate, gate + (size_t)I * H, tile, (size_t)(g.gpre[u] + kSbSlice * sj) * I, ms, tok, sm.up.bt,
+                sm.up.at);
 }
 
 // Down: one wave per (slice, 32 output columns); the slice comes from the up kernel's
@@ -668,7 +767,8 @@ __global__ __launch_bounds__(64) void k_sb_down(SbParams p) {
 // blocks spread the router weight's read over E / 4 CUs per token (4-wave blocks, a quarter as
 // many CUs: T=2 63.4 against 62.7 us per layer).  Blocks (t, y >= nb), when sp.sh_pre, run the
 // shared expert's up tiles and gate, which need no routing: (y - nb) T + t indexes the shared
-// slices' tiles (R stages in flight), and tile indexes below T compute token j's gate.
+// slices' tiles of 4 activation columns (R stages in flight, so a tile is two ring lengths and
+// ends within the routing's latency), and tile indexes below T compute token j's gate.
 template <int MAXC, int MAXEPL, int R>
 __global__ __launch_bounds__(64 * kSbRouterWaves) void k_sb_router(const uint16_t* __restrict__ x,
                                                                    const uint16_t* __restrict__ wg, int H, int E,
@@ -680,9 +780,9 @@ __global__ __launch_bounds__(64 * kSbRouterWaves) void k_sb_router(const uint16_
   __shared__ int last;
   if ((int)blockIdx.y >= nb) {
     __shared__ u32x4 bt[16 * 17], at[8 * 17];
-    const int j = ((int)blockIdx.y - nb) * (int)gridDim.x + t, tiles = sp.I / 8;
+    const int j = ((int)blockIdx.y - nb) * (int)gridDim.x + t, tiles = sp.I / 4;
     const int sj = j / tiles;
-    if (sj < (sp.T + kSbSlice - 1) / kSbSlice) sb_shared_up<R>(sp, sj, j - sj * tiles, j, bt, at);
+    if (sj < (sp.T + kSbSlice - 1) / kSbSlice) sb_shared_up<R, 4>(sp, sj, j - sj * tiles, j, bt, at);
     return;
   }
   XFrag<MAXC> xf;
@@ -731,34 +831,34 @@ bool sb_supported(int T, int H, int I, int Is, int k, int q4) {
 }
 
 static void sb_launch_up(const SbParams& p, int R, dim3 grid, hipStream_t s) {
-  const bool shd = p.sh_pre != 0;   // only with R = 4 or 5 (sb_shared_pre)
+  if (p.sh_pre) {   // R = 4 or 5 (sb_shared_pre)
+    if (R == 5) hipLaunchKernelGGL((k_sb_up_shd<5>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((k_sb_up_shd<4>), grid, dim3(64), 0, s, p);
+    return;
+  }
   switch (R) {
-    case 5:
-      if (shd) hipLaunchKernelGGL((k_sb_up<5, true>), grid, dim3(64), 0, s, p);
-      else hipLaunchKernelGGL((k_sb_up<5, false>), grid, dim3(64), 0, s, p);
-      break;
-    case 4:
-      if (shd) hipLaunchKernelGGL((k_sb_up<4, true>), grid, dim3(64), 0, s, p);
-      else hipLaunchKernelGGL((k_sb_up<4, false>), grid, dim3(64), 0, s, p);
-      break;
-    case 3: hipLaunchKernelGGL((k_sb_up<3, false>), grid, dim3(64), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((k_sb_up<2, false>), grid, dim3(64), 0, s, p); break;
-    default: hipLaunchKernelGGL((k_sb_up<1, false>), grid, dim3(64), 0, s, p); break;
+    case 5: hipLaunchKernelGGL((k_sb_up<5>), grid, dim3(64), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((k_sb_up<4>), grid, dim3(64), 0, s, p); break;
+    case 3: hipLaunchKernelGGL((k_sb_up<3>), grid, dim3(64), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((k_sb_up<2>), grid, dim3(64), 0, s, p); break;
+    default: hipLaunchKernelGGL((k_sb_up<1>), grid, dim3(64), 0, s, p); break;
   }
 }
 
 // Whether the router launch can take the shared expert's gate/up (and the up launch its down):
-// a shared expert, up tiles of 4 or 5 stages in flight, down tiles of 2, E <= 256.
+// a shared expert, up tiles of 4 or 5 stages in flight in the up launch and of 8 or 10 in the
+// router launch, down tiles of 2, E <= 256.
 static bool sb_shared_pre(bool has_sh, int H, int E, int I) {
-  const int r = sb_ring(H / 128, 5);
-  return has_sh && (r == 4 || r == 5) && sb_ring(I / 128, 2) == 2 && E <= 256;
+  const int r = sb_ring(H / 128, 5), rs = sb_ring(H / 128, 10);
+  return has_sh && (r == 4 || r == 5) && (rs == 8 || rs == 10) && sb_ring(I / 128, 2) == 2 && E <= 256;
 }
 // Token counts that take it.  Full-size layer (H=2560, E=256, I=1024, k=8, 8 rotating layers,
-// same-run A/B, three rounds): T=2 62.6-62.9 -> 61.1-61.4 us (router 7.6 -> 8.5, up 31.7 -> 30.5,
-// down 23.8 -> 22.4); T=4 95.5 -> 97.0, T=8 156.4 -> 159.5, T=16 260 -> 263-266: with more
-// tokens the shared slice is a smaller part of the up and down launches, and the router launch
-// then waits for its shared tiles (each wave streams 80 KB in four ring lengths, ~8 us; a
-// delay before them made T=2 slower still: 62.1 / 62.9 / 64.6 us for ~1 / 2 / 4 us).
+// same-run A/B, three rounds each): T=2 62.5-62.6 -> 60.2-60.5 us per layer; the same relocation
+// at every T was slower from T=3 on (T=3 77.3 -> 77.5-77.7, T=4 94.4 -> 94.8-95.1, T=8 154.6 ->
+// 156.0-156.4, T=16 259.0 -> 262.7-263.1): the shared slice is a smaller part of the up and down
+// launches there, and the router launch waits for its shared tiles.  Shared tiles of 8 columns
+// (5 stages in flight, four ring lengths of 80 KB) gave 61.1-61.4 at T=2 (router 7.6 -> 8.5 us);
+// a delay before them made it slower still (62.1 / 62.9 / 64.6 us for ~1 / 2 / 4 us).
 static bool sb_shared_pre_tokens(int T) { return T == 2; }
 
 static SbParams sb_params(const uint16_t* x, int T, const uint16_t* sh_gate, const uint16_t* sh_up,
@@ -839,14 +939,14 @@ int sb_router_launch(const uint16_t* x, const uint16_t* wg, int T, int H, int E,
                    sb_shared_pre(sh_gate != nullptr, H, E, I);
   SbParams sp = sb_params(x, T, sh_gate, sh_up, nullptr, sh_gate_w, H, E, I, k, Is, ws);
   const int nb = (E + 4 * kSbRouterWaves - 1) / (4 * kSbRouterWaves);
-  const int shared_tiles = pre ? (T + kSbSlice - 1) / kSbSlice * (I / 8) : 0;
+  const int shared_tiles = pre ? (T + kSbSlice - 1) / kSbSlice * (I / 4) : 0;
   const dim3 g(T, nb + (shared_tiles + T - 1) / T), b(64 * kSbRouterWaves);
   const int nc = (H + 511) / 512;
-  const bool r5 = sb_ring(H / 128, 5) == 5;
-#define TMOE_SB_ROUTER(MAXC)                                                                                   \
-  if (E > 256) hipLaunchKernelGGL((k_sb_router<MAXC, 16, 4>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp); \
-  else if (r5) hipLaunchKernelGGL((k_sb_router<MAXC, 4, 5>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp);  \
-  else hipLaunchKernelGGL((k_sb_router<MAXC, 4, 4>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp);
+  const bool r10 = sb_ring(H / 128, 10) == 10;
+#define TMOE_SB_ROUTER(MAXC)                                                                                    \
+  if (E > 256) hipLaunchKernelGGL((k_sb_router<MAXC, 16, 8>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp); \
+  else if (r10) hipLaunchKernelGGL((k_sb_router<MAXC, 4, 10>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp); \
+  else hipLaunchKernelGGL((k_sb_router<MAXC, 4, 8>), g, b, 0, s, x, wg, H, E, k, nb, logits, cnt, o, sp);
   switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
     case 2: TMOE_SB_ROUTER(2) break;
     case 4: TMOE_SB_ROUTER(4) break;
