@@ -17,7 +17,9 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
                    const uint16_t* wb, const uint64_t* table, const uint16_t* sh_gate, const uint16_t* sh_up,
                    const uint16_t* sh_down, const float* gs, int H, int E, int I, int k, int Is, uint16_t* out,
                    void* ws, hipStream_t s, int q4, const uint16_t* resid, uint32_t* err);
-int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s);
+int launch_router_topk_gate(const float* logits, int T, int E, int k, int64_t* ids64, uint16_t* wb, int32_t* ids32,
+                            float* wf, uint32_t* heat, const uint16_t* x, const uint16_t* w_sg, int H, float* gs,
+                            hipStream_t s);
 int rmsnorm_launch(const uint16_t* h, const uint16_t* w, float eps, int T, int H, uint16_t* x, hipStream_t s);
 int residual_add_launch(const uint16_t* h, uint16_t* y, size_t n, hipStream_t s);
 bool sb_supported(int T, int H, int I, int Is, int k, int q4);
@@ -260,9 +262,14 @@ static int moe_block(const void* x, int T, const void* router_w, const float* lo
     if (int st = launch_router_logits((const uint16_t*)x, (const uint16_t*)router_w, T, H, E, logits, s)) return st;
     lg = logits;
   }
-  if (int st = launch_router_topk(lg, T, E, k, ids_out, (uint16_t*)weights_out, ids32, wf, heat, s)) return st;
-  if (has_sh)
-    if (int st = launch_shared_gate((const uint16_t*)x, (const uint16_t*)sh_gate_w, T, H, gs, s)) return st;
+  // Top-k and, with a shared expert, its gate in the same launch.
+  if (has_sh) {
+    if (int st = launch_router_topk_gate(lg, T, E, k, ids_out, (uint16_t*)weights_out, ids32, wf, heat,
+                                         (const uint16_t*)x, (const uint16_t*)sh_gate_w, H, gs, s))
+      return st;
+  } else if (int st = launch_router_topk(lg, T, E, k, ids_out, (uint16_t*)weights_out, ids32, wf, heat, s)) {
+    return st;
+  }
   return prefill_launch((const uint16_t*)x, T, ids32, nullptr, wf, nullptr, expert_table, (const uint16_t*)sh_gate,
                         (const uint16_t*)sh_up, (const uint16_t*)sh_down, has_sh ? gs : nullptr, H, E, I, k, Is,
                         (uint16_t*)out, workspace, s, q4, ln_w ? (const uint16_t*)h : nullptr, err);

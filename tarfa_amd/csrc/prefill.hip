@@ -31,32 +31,15 @@ constexpr int kRing = 3;        // K stages of A and of the weights requested ah
 __device__ __forceinline__ int load_id(const int32_t* ids32, const int64_t* ids64, size_t i) {
   return ids32 ? ids32[i] : (int)ids64[i];
 }
-
-// ---------------------------------------------------------------- shared gate
-template <int MAXC>
-__global__ __launch_bounds__(256) void k_shared_gate(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wsg,
-                                                     int T, int H, float* __restrict__ gs) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  XFrag<MAXC> xf;
-  load_xfrag<MAXC>(xf, x + (size_t)t * H, H, lane);
-  const uint16_t* rows[1] = {wsg};
-  float d[1];
-  wave_dots<MAXC, 1>(rows, xf, H, lane, d);
-  if (lane == 0) gs[t] = rbf16(sigmoid_f32(rbf16(d[0])));
+// Ids 4q .. 4q + 3 with 16-byte loads (the pointer 16-byte aligned).
+__device__ __forceinline__ int4 load_id4(const int32_t* ids32, const int64_t* ids64, size_t q) {
+  if (ids32) return *reinterpret_cast<const int4*>(ids32 + 4 * q);
+  const longlong2 a = *reinterpret_cast<const longlong2*>(ids64 + 4 * q);
+  const longlong2 b = *reinterpret_cast<const longlong2*>(ids64 + 4 * q + 2);
+  return int4{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
 }
-
-int launch_shared_gate(const uint16_t* x, const uint16_t* w_sg, int T, int H, float* gs, hipStream_t s) {
-  const int nc = (H + 511) / 512;
-  const dim3 g((T + 3) / 4), b(256);
-  switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
-    case 2: hipLaunchKernelGGL(k_shared_gate<2>, g, b, 0, s, x, w_sg, T, H, gs); break;
-    case 4: hipLaunchKernelGGL(k_shared_gate<4>, g, b, 0, s, x, w_sg, T, H, gs); break;
-    case 6: hipLaunchKernelGGL(k_shared_gate<6>, g, b, 0, s, x, w_sg, T, H, gs); break;
-    default: hipLaunchKernelGGL(k_shared_gate<8>, g, b, 0, s, x, w_sg, T, H, gs); break;
-  }
-  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+__device__ __forceinline__ bool ids_aligned(const int32_t* ids32, const int64_t* ids64) {
+  return ((ids32 ? (uintptr_t)ids32 : (uintptr_t)ids64) & 15u) == 0;
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -72,19 +55,31 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const int32_t* ids32, c
   __syncthreads();
   const int n = T * k;
   bool bad = false;
-  for (int j0 = tid; j0 < n; j0 += 8 * 1024) {       // 8 independent loads in flight per thread
-    int ev[8];
+  auto take = [&](int e) {
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    else if (e != E) bad = true;
+  };
+  // Four ids per 16-byte load, 8 loads in flight per thread (T=4096, k=8: one round trip), when
+  // the ids and inv are 16-byte aligned; the remainder one at a time.
+  const int nq = ids_aligned(ids32, ids64) && ((uintptr_t)inv & 15u) == 0 ? n / 4 : 0;
+  for (int q0 = tid; q0 < nq; q0 += 8 * 1024) {
+    int4 ev[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) ev[u] = j0 + u * 1024 < n ? load_id(ids32, ids64, j0 + u * 1024) : E;
+    for (int u = 0; u < 8; ++u) ev[u] = q0 + u * 1024 < nq ? load_id4(ids32, ids64, q0 + u * 1024) : int4{E, E, E, E};
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int j = j0 + u * 1024;
-      if (j >= n) continue;
-      const int e = ev[u];
-      if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-      else if (e != E) bad = true;
-      inv[j] = -1;
+      const int q = q0 + u * 1024;
+      if (q >= nq) continue;
+      take(ev[u].x);
+      take(ev[u].y);
+      take(ev[u].z);
+      take(ev[u].w);
+      reinterpret_cast<int4*>(inv)[q] = int4{-1, -1, -1, -1};
     }
+  }
+  for (int j = 4 * nq + tid; j < n; j += 1024) {
+    take(load_id(ids32, ids64, j));
+    inv[j] = -1;
   }
   if (bad && err) atomicOr(err, 1u);
   __syncthreads();
@@ -141,17 +136,27 @@ __global__ __launch_bounds__(1024) void k_dispatch_scatter(const int32_t* ids32,
   const int nw = (n + 31) / 32;
   for (int w = tid; w < nw; w += 1024) mask[w] = 0u;
   __syncthreads();
-  for (int i0 = tid; i0 < n; i0 += 8 * 1024) {       // 8 independent loads in flight per thread
-    int ev[8];
+  auto mark = [&](int i) {
+    const int t = i / k, slot = i - t * k, j = slot * T + t;
+    atomicOr(&mask[j >> 5], 1u << (j & 31));
+  };
+  // Four ids per 16-byte load, 8 loads in flight per thread, when aligned; the rest one at a time.
+  const int nq = ids_aligned(ids32, ids64) ? n / 4 : 0;
+  for (int q0 = tid; q0 < nq; q0 += 8 * 1024) {
+    int4 ev[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) ev[u] = i0 + u * 1024 < n ? load_id(ids32, ids64, i0 + u * 1024) : -1;
+    for (int u = 0; u < 8; ++u) ev[u] = q0 + u * 1024 < nq ? load_id4(ids32, ids64, q0 + u * 1024) : int4{-1, -1, -1, -1};
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      if (ev[u] != e) continue;
-      const int i = i0 + u * 1024, t = i / k, slot = i - t * k, j = slot * T + t;
-      atomicOr(&mask[j >> 5], 1u << (j & 31));
+      const int i = 4 * (q0 + u * 1024);
+      if (ev[u].x == e) mark(i);
+      if (ev[u].y == e) mark(i + 1);
+      if (ev[u].z == e) mark(i + 2);
+      if (ev[u].w == e) mark(i + 3);
     }
   }
+  for (int i = 4 * nq + tid; i < n; i += 1024)
+    if (load_id(ids32, ids64, i) == e) mark(i);
   __syncthreads();
   const int wpt = (nw + 1023) / 1024;
   const int w_lo = min(nw, tid * wpt), w_hi = min(nw, w_lo + wpt);

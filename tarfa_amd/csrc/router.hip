@@ -156,6 +156,68 @@ int launch_router_logits(const uint16_t* x, const uint16_t* wg, int T, int H, in
   return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
 }
 
+// The same top-k with the shared expert's gate beside it: wave t also computes
+// gs[t] = bf16(sigmoid(bf16(x_t . w_sg))) (fp32 products of the bf16 values, lane l summing
+// columns 512 c + 8 l .. + 7 over c in order, then the wave sum), its x row and the gate row
+// requested before the logits so both round trips overlap: one launch where a separate
+// shared-gate GEMV took a second.
+template <int MAXEPL, int MAXC>
+__global__ __launch_bounds__(256) void k_router_topk_gate(const float* __restrict__ logits, int T, int E, int k,
+                                                          int64_t* ids64, uint16_t* wb, int32_t* ids32, float* wf,
+                                                          uint32_t* heat, const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ wsg, int H,
+                                                          float* __restrict__ gs) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  u32x4 xr[MAXC], w[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int col = c * 512 + lane * 8;
+    xr[c] = col < H ? ld16(x + (size_t)t * H + col) : u32x4{0u, 0u, 0u, 0u};
+    w[c] = col < H ? ld_stream(wsg + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+  TopkOut o;
+  o.ids32 = ids32 ? ids32 + (size_t)t * k : nullptr;
+  o.wf = wf ? wf + (size_t)t * k : nullptr;
+  o.ids64 = ids64 ? ids64 + (size_t)t * k : nullptr;
+  o.wb = wb ? wb + (size_t)t * k : nullptr;
+  o.heat = heat;
+  wave_topk<MAXEPL>(logits + (size_t)t * E, false, E, k, lane, o);
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const float xv[8] = {bf16_lo(xr[c].x), bf16_hi(xr[c].x), bf16_lo(xr[c].y), bf16_hi(xr[c].y),
+                         bf16_lo(xr[c].z), bf16_hi(xr[c].z), bf16_lo(xr[c].w), bf16_hi(xr[c].w)};
+    acc = dot8(w[c], xv, acc);
+  }
+  const float d = wave_sum(acc);
+  if (lane == 0) gs[t] = rbf16(sigmoid_f32(rbf16(d)));
+}
+
+int launch_router_topk_gate(const float* logits, int T, int E, int k, int64_t* ids64, uint16_t* wb, int32_t* ids32,
+                            float* wf, uint32_t* heat, const uint16_t* x, const uint16_t* w_sg, int H, float* gs,
+                            hipStream_t s) {
+  const dim3 grid((T + 3) / 4), block(256);
+  const bool small_e = (E + 63) / 64 <= 4;
+  const int nc = (H + 511) / 512;
+#define TMOE_TOPK_GATE(MAXC)                                                                                      \
+  if (small_e)                                                                                                    \
+    hipLaunchKernelGGL((k_router_topk_gate<4, MAXC>), grid, block, 0, s, logits, T, E, k, ids64, wb, ids32, wf,    \
+                       heat, x, w_sg, H, gs);                                                                     \
+  else                                                                                                            \
+    hipLaunchKernelGGL((k_router_topk_gate<16, MAXC>), grid, block, 0, s, logits, T, E, k, ids64, wb, ids32, wf,   \
+                       heat, x, w_sg, H, gs);
+  switch (nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 6 ? 6 : 8) {
+    case 2: TMOE_TOPK_GATE(2) break;
+    case 4: TMOE_TOPK_GATE(4) break;
+    case 6: TMOE_TOPK_GATE(6) break;
+    default: TMOE_TOPK_GATE(8) break;
+  }
+#undef TMOE_TOPK_GATE
+  return hipGetLastError() == hipSuccess ? TMOE_OK : TMOE_ERR_HIP;
+}
+
 int launch_router_topk(const float* logits, int T, int E, int k, int64_t* ids64, uint16_t* wb, int32_t* ids32,
                        float* wf, uint32_t* heat, hipStream_t s) {
   const dim3 grid((T + 3) / 4), block(256);
