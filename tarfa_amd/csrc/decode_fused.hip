@@ -667,8 +667,8 @@ __device__ __forceinline__ void task_router(const DecodeParams& p, int t, int la
 // The words a D(k-1) task combines (lane r < 8: its row h0 + r of each earlier slot, then
 // of the shared expert; clamped addresses), one batch of loads after the task's own rows.
 // (Requested before the rows, to overlap the round trip, they cost the exact-bf16 call
-// 0.2-0.5 us in a same-run A/B, while the int4 mode, whose down tasks are shorter, gains
-// 0.8 us that way: combine_words_q4.)
+// 0.2-0.5 us in a same-run A/B, and between the rows and the activations 0.3-0.8 us, while
+// the int4 mode, whose down tasks are shorter, gains 0.8 us that way: combine_words_q4.)
 __device__ __forceinline__ void combine_words(const DecodeParams& p, int h0, int lane, uint64_t (&v)[kFusedMaxK]) {
   const int r = lane & (kDownRows - 1);
 #pragma unroll
