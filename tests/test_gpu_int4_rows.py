@@ -132,6 +132,33 @@ def test_rows_prefill_matches_bf16_chain_on_dequantised_weights(gpu, T):
     assert_close_bf16(f32(out2), ref2, f"int4 rows experts T={T}")
 
 
+def test_rows_prefill_full_size_sampled_tokens(gpu):
+    """The per-row-scale prefill GEMM at the full-size layer (H=2560, E=256, I=1024, shared
+    expert), T = 300: every token's ids against the oracle router, and 12 sampled tokens'
+    outputs against the exact-BF16 chain on the dequantised weights of the experts they use."""
+    shape, T = FULL, 300
+    layer = seeded.make_layer(shape, 61, device=gpu)
+    q = rows_layer(layer)
+    table = tm.expert_table_q4_rows(*q)
+    ws = Workspace(shape, gpu, tokens=T)
+    x = seeded.make_tokens(shape, 61, T, device=gpu)
+    logits = seeded.make_logits(shape, 61, T, device=gpu)
+    out, ids, w = tm.moe_block(shape, x, table, ws, logits=logits, shared=layer.shared)
+    torch.cuda.synchronize()
+    ws.status()
+    ids_d = ids.cpu().numpy()
+    ids_ref, _, _ = moe.router_topk(logits.cpu().numpy(), shape.top_k)
+    assert np.array_equal(ids_d, ids_ref)
+    pick = np.linspace(0, T - 1, 12).astype(int)
+    sel = ids_d[pick]
+    gu = {e: bf16.to_f32(int4.dequant_rows_bf16(q[0][e].cpu().numpy(), u16(q[1][e]))) for e in set(sel.ravel().tolist())}
+    dn = {e: bf16.to_f32(int4.dequant_rows_bf16(q[2][e].cpu().numpy(), u16(q[3][e]))) for e in gu}
+    xs = f32(x)[pick]
+    ref = moe.experts_prefill(xs, sel, f32(w)[pick], gu, dn, shape.num_experts)
+    ref = moe.add_bf16(ref, moe.shared_expert(xs, *[f32(t) for t in layer.shared]))
+    assert_close_bf16(f32(out)[pick], ref, f"int4 rows prefill full size T={T}")
+
+
 def test_rows_prefill_register_staged_kernel(gpu):
     """A shape the persistent GEMM does not take (H = 640, I = 384): the register-staged
     kernel's per-row-scale path."""
