@@ -236,6 +236,26 @@ def test_prefill_small_block(gpu, T, shared):
     assert_close_bf16(f32(out2), ref2, f"prefill experts T={T}")
 
 
+def test_prefill_many_experts_with_shared_gate(gpu):
+    """E = 300 (the top-k's 16-logits-per-lane variant) with a shared expert at T = 40: the
+    top-k and the shared gate run in one launch; ids exact, outputs at the bf16 bars."""
+    shape = MoEShape(256, 300, 128, 6, 128)
+    T = 40
+    layer = seeded.make_layer(shape, 83, device=gpu)
+    ws = Workspace(shape, gpu, tokens=T)
+    table = tm.expert_table(layer.gate_up, layer.down)
+    x = seeded.make_tokens(shape, 83, T, device=gpu)
+    logits = seeded.make_logits(shape, 83, T, device=gpu)
+    out, ids, w = tm.moe_block(shape, x, table, ws, logits=logits, shared=layer.shared)
+    ids_ref, w_ref, _ = moe.router_topk(logits.cpu().numpy(), shape.top_k)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    xs = f32(x)
+    gu, dn = expert_dicts(layer.gate_up, layer.down, ids_ref)
+    ref = moe.add_bf16(moe.experts_prefill(xs, ids_ref, f32(w), gu, dn, shape.num_experts),
+                       moe.shared_expert(xs, *[f32(t) for t in layer.shared]))
+    assert_close_bf16(f32(out), ref, "prefill E=300 with shared gate")
+
+
 def test_prefill_group_larger_than_one_tile(gpu):
     """Skewed routing: one expert receives every token (> 256 rows -> several M-chunks)."""
     shape = MoEShape(256, 8, 128, 2)
