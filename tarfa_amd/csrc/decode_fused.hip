@@ -944,10 +944,15 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   // first waited for where a task stores or polls.
   const uint32_t tag = ld32c(queue + kQueueEpochWord) + 1u;
   __shared__ RouteLds s_rt;     // the block's view of the routing
+  // LN: the block's normalised input, formed by one of its waves (s_xstate 0 -> 1 claimed -> 2
+  // published in s_x); the others copy it.
+  __shared__ u32x4 s_x[LN ? MH * 64 : 1];
+  __shared__ uint32_t s_xstate;
   if (threadIdx.x == 0) {
     s_rt.valid = 0u;
     s_rt.wvalid = 0u;
     s_rt.poller = 0u;
+    s_xstate = 0u;
   }
   __syncthreads();
 
@@ -968,10 +973,35 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   // wave reduction over h) and kept in registers for the wave's later tasks.
   XPack<MH> xcache;
   bool have_x = false;
+  // LN: the first wave of the block to claim the input forms it and publishes it in LDS; a wave
+  // that finds it claimed copies it once published (the claimer's loads and norm are bounded).
+  // One norm per block instead of per wave: 2048 waves each reading h and the norm weight at
+  // entry queued the router rows' loads behind 20 MB of requests (router loads 3.3 -> 1.4 us,
+  // routing resolved 10.0 -> 8.7 us in the per-task timeline; layer 36.2-36.8 -> 36.1-36.5 us).
+  // Only lane 0 takes part in the claim.
+  auto claim_x = [&](int lane) {
+    uint32_t st = 0;
+    if (lane == 0) st = atomicCAS(&s_xstate, 0u, 1u);
+    return __builtin_amdgcn_readfirstlane((int)st) == 0;
+  };
+  auto form_x = [&](int lane) {
+    load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane);
+#pragma unroll
+    for (int c = 0; c < MH; ++c) s_x[c * 64 + lane] = xcache.v[c];
+    __hip_atomic_store(&s_xstate, 2u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
   auto get_x = [&](XPack<MH>& xf, int lane) {
     if constexpr (LN) {
       if (!have_x) {
-        load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane);
+        if (claim_x(lane)) {
+          form_x(lane);
+        } else {
+          Backoff<4> b;
+          while (__hip_atomic_load(&s_xstate, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 2u)
+            if (!b.step(err)) break;
+#pragma unroll
+          for (int c = 0; c < MH; ++c) xcache.v[c] = s_x[c * 64 + lane];
+        }
         have_x = true;
       }
       xf = xcache;
@@ -986,8 +1016,8 @@ __global__ __launch_bounds__(256, 2) void k_decode_fused(DecodeParams p) {
   // static tickets, left the waves that drew another wave's planned router task to form x on
   // first use: 39.1-39.2 against 37.9-38.2 us per layer.
   if constexpr (LN) {
-    if (q + NQ * (int)ticket >= p.n_r) {
-      load_xpack_norm<MH, EXACT>(xcache, p.x, p.ln_w, p.ln_eps, p.H, lane0);
+    if (q + NQ * (int)ticket >= p.n_r && claim_x(lane0)) {
+      form_x(lane0);
       have_x = true;
     }
   }
