@@ -328,59 +328,106 @@ struct SbOrderRegs {
   }
 };
 
-// Combine of output columns [c0, c0 + ncols) for every token, one lane per (token, 8
+// W 32-bit words (2 W bf16 columns) of a row: agent-scope loads (the other waves' outputs) or
+// plain ones (the residual), and the store.
+template <int W>
+struct SbWords {
+  uint32_t v[W];
+};
+template <int W>
+__device__ __forceinline__ SbWords<W> sb_ld_words_coherent(const uint16_t* p) {
+  SbWords<W> r;
+  if constexpr (W == 4) {
+    const u32x4 q = sb_ld_coherent(p);
+    r.v[0] = q.x; r.v[1] = q.y; r.v[2] = q.z; r.v[3] = q.w;
+  } else if constexpr (W == 2) {
+    const uint64_t q = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    r.v[0] = (uint32_t)q; r.v[1] = (uint32_t)(q >> 32);
+  } else {
+    static_assert(W == 1, "1, 2 or 4 words");
+    r.v[0] = __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return r;
+}
+template <int W>
+__device__ __forceinline__ SbWords<W> sb_ld_words(const uint16_t* p) {
+  SbWords<W> r;
+  if constexpr (W == 4) {
+    const u32x4 q = ld16(p);
+    r.v[0] = q.x; r.v[1] = q.y; r.v[2] = q.z; r.v[3] = q.w;
+  } else if constexpr (W == 2) {
+    const uint64_t q = *reinterpret_cast<const uint64_t*>(p);
+    r.v[0] = (uint32_t)q; r.v[1] = (uint32_t)(q >> 32);
+  } else {
+    r.v[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+  return r;
+}
+
+// Combine of output columns [c0, c0 + ncols) for every token, one lane per (token, 2 W
 // columns): the shared expert's output, the residual and up to 8 expert outputs (agent-scope
-// loads) requested together, then added in rank order.
-__device__ void sb_combine(const SbParams& p, const SbOrder& o, int c0, int ncols) {
-  const int H = p.H, k = p.k, chunks = ncols / 8;
+// loads) requested together, then added in rank order.  acc = bf16(acc + bf16(x * w)) per
+// column, the roundings two columns per hardware conversion (round to nearest even, as the
+// bit-operation form, which made the combine VALU-bound: ~4.5 us for the last wave of a tile at
+// T=2 in a per-wave timeline, 2.4 us with the conversions and 8 columns per lane).
+template <int W>
+__device__ void sb_combine_w(const SbParams& p, const SbOrder& o, int c0, int ncols) {
+  const int H = p.H, k = p.k, chunks = ncols / (2 * W);
   for (int job = threadIdx.x; job < p.T * chunks; job += blockDim.x) {
-    const int t = job / chunks, col = c0 + (job - t * chunks) * 8;
+    const int t = job / chunks, col = c0 + (job - t * chunks) * 2 * W;
     const int nv = o.n[t];
-    const u32x4 vs = p.sh_gate ? sb_ld_coherent(p.sh + (size_t)t * H + col) : u32x4{0u, 0u, 0u, 0u};
-    const u32x4 hv = p.resid ? ld16(p.resid + (size_t)t * H + col) : u32x4{0u, 0u, 0u, 0u};
-    float acc[8];
+    SbWords<W> vs{}, hv{};
+    if (p.sh_gate) vs = sb_ld_words_coherent<W>(p.sh + (size_t)t * H + col);
+    if (p.resid) hv = sb_ld_words<W>(p.resid + (size_t)t * H + col);
+    float acc[2 * W];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    // acc = bf16(acc + bf16(x * w)) per column; the roundings two columns per hardware
-    // conversion (round to nearest even, as the bit-operation form, which made the combine
-    // VALU-bound: ~4.5 us for the last wave of a tile at T=2, in a per-wave timeline).
-    auto add = [&](const u32x4 d, float wgt) {
-      const float x[8] = {bf16_lo(d.x), bf16_hi(d.x), bf16_lo(d.y), bf16_hi(d.y),
-                          bf16_lo(d.z), bf16_hi(d.z), bf16_lo(d.w), bf16_hi(d.w)};
+    for (int i = 0; i < 2 * W; ++i) acc[i] = 0.f;
+    auto add = [&](const SbWords<W>& d, float wgt) {
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        float p0 = x[i] * wgt, p1 = x[i + 1] * wgt;
+      for (int i = 0; i < W; ++i) {
+        float p0 = bf16_lo(d.v[i]) * wgt, p1 = bf16_hi(d.v[i]) * wgt;
         rbf16x2_hw(p0, p1);
-        float s0 = acc[i] + p0, s1 = acc[i + 1] + p1;
+        float s0 = acc[2 * i] + p0, s1 = acc[2 * i + 1] + p1;
         rbf16x2_hw(s0, s1);
-        acc[i] = s0;
-        acc[i + 1] = s1;
+        acc[2 * i] = s0;
+        acc[2 * i + 1] = s1;
       }
     };
     // Eight entries' loads in flight at a time, added in rank order.
     for (int j0 = 0; j0 < nv; j0 += 8) {
-      u32x4 v[8];
+      SbWords<W> v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (j0 + j < nv) v[j] = sb_ld_coherent(p.ch + (size_t)o.row[t * k + j0 + j] * H + col);
+        if (j0 + j < nv) v[j] = sb_ld_words_coherent<W>(p.ch + (size_t)o.row[t * k + j0 + j] * H + col);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (j0 + j < nv) add(v[j], o.w[t * k + j0 + j]);
     }
     if (p.sh_gate) add(vs, o.gs[t]);
-    if (p.resid) {   // the layer's residual add: bf16(h + y)
-      const float hx[8] = {bf16_lo(hv.x), bf16_hi(hv.x), bf16_lo(hv.y), bf16_hi(hv.y),
-                           bf16_lo(hv.z), bf16_hi(hv.z), bf16_lo(hv.w), bf16_hi(hv.w)};
+    SbWords<W> out;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = hx[i] + acc[i];
+    for (int i = 0; i < W; ++i) {
+      float a = acc[2 * i], b = acc[2 * i + 1];
+      if (p.resid) {   // the layer's residual add: bf16(h + y)
+        a = bf16_lo(hv.v[i]) + a;
+        b = bf16_hi(hv.v[i]) + b;
+      }
+      out.v[i] = bf16x2_bits_hw(a, b);
     }
-    u32x4 out;
-    out.x = bf16x2_bits_hw(acc[0], acc[1]);
-    out.y = bf16x2_bits_hw(acc[2], acc[3]);
-    out.z = bf16x2_bits_hw(acc[4], acc[5]);
-    out.w = bf16x2_bits_hw(acc[6], acc[7]);
-    *reinterpret_cast<u32x4*>(p.out + (size_t)t * H + col) = out;
+    uint16_t* dst = p.out + (size_t)t * H + col;
+    if constexpr (W == 4) *reinterpret_cast<u32x4*>(dst) = u32x4{out.v[0], out.v[1], out.v[2], out.v[3]};
+    else if constexpr (W == 2) *reinterpret_cast<uint64_t*>(dst) = (uint64_t)out.v[0] | ((uint64_t)out.v[1] << 32);
+    else *reinterpret_cast<uint32_t*>(dst) = out.v[0];
   }
+}
+// The fewest columns per lane that still cover the tile in one pass of the wave (each pass is a
+// round trip of loads): T = 2 two columns per lane (1.4 us less per call than eight), T = 3, 4
+// four, else eight (two columns at T = 4 took two passes: +0.4 us).
+__device__ void sb_combine(const SbParams& p, const SbOrder& o, int c0, int ncols) {
+  if (p.T * (ncols / 2) <= 64) sb_combine_w<1>(p, o, c0, ncols);
+  else if (p.T * (ncols / 4) <= 64) sb_combine_w<2>(p, o, c0, ncols);
+  else sb_combine_w<4>(p, o, c0, ncols);
 }
 
 // Up work of one (slice, NC activation columns) tile: NC gate and NC up weight rows over K = H
