@@ -536,6 +536,11 @@ __device__ __forceinline__ u32x4 gld16(const void* sbase, uint32_t voff) {
   asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
   return v;
 }
+__device__ __forceinline__ u32x2 gld8(const void* sbase, uint32_t voff) {
+  u32x2 v;
+  asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
+  return v;
+}
 __device__ __forceinline__ uint32_t gld4(const void* sbase, uint32_t voff) {
   uint32_t v;
   asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase));
@@ -588,6 +593,8 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = p.K;
   const int cols = p.up ? kPUpCols : kPDnCols;
+  // B stages in flight.  Int4: 8 (a stage is 2 KB per wave: with 4, ~1 TB/s of weights).
+  constexpr int kB = Q4 ? kPR : kPB;
 
   // Tiles f = (M-chunk - c_lo) * n_ntiles + N-tile.  XCD x (blocks b with b % 8 == x) takes
   // the contiguous range [x per_xcd, (x + 1) per_xcd); its blocks interleave over it, so the
@@ -650,6 +657,10 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 
   // Lane constants.  A: load j of this wave covers rows 8 x .. 8 x + 7 (x = wid + 8 j, the
   // last four repeating 16..19); B: row lane % 16 of each block, k offset 8 (lane / 16).
+  // Int4: lane group g = lane / 16 loads bytes 8 g .. 8 g + 7 of its row's 32-byte stage (k
+  // 16 g .. 16 g + 15) in one instruction, the first four bytes its fragment of k step 0 and
+  // the last four of k step 1; its A fragments are then 16-byte chunks 2 g and 2 g + 1 of the
+  // stage, the same k values (a permutation of k within the stage, applied to both operands).
   const int lrow = lane & 15, lk = 8 * (lane >> 4);
   int a_row[kPLoads];
 #pragma unroll
@@ -658,8 +669,9 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
     a_row[j] = 8 * (x < kBM / 8 ? x : x - kPW / 2) + (lane >> 3);
   }
   const int a_col = 8 * ((lane & 7) ^ (lane >> 3));
-  const int a_rd0 = lrow * 8 + ((lane >> 4) ^ (lrow & 7));
-  const int a_rd1 = lrow * 8 + ((4 + (lane >> 4)) ^ (lrow & 7));
+  const int a_ch0 = Q4 ? 2 * (lane >> 4) : lane >> 4, a_ch1 = Q4 ? 2 * (lane >> 4) + 1 : 4 + (lane >> 4);
+  const int a_rd0 = lrow * 8 + (a_ch0 ^ (lrow & 7));
+  const int a_rd1 = lrow * 8 + (a_ch1 ^ (lrow & 7));
 
   f32x4 acc[kPMB][kPNB];
   auto zero_acc = [&]() {
@@ -670,8 +682,8 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   };
   zero_acc();
 
-  u32x4 breg[kPB][kPNB][2];
-  uint32_t qreg[kPB][kPNB][2], sreg[kPB][kPNB];
+  u32x4 breg[Q4 ? 1 : kB][kPNB][2];
+  uint32_t qreg[kB][kPNB][2], sreg[kB][kPNB];
   const int nk = K / kBK;   // a multiple of kPR
   // Stage st of tile cur, or (nx) stage st of tile nxt: the pointers are selected, not
   // branched on, so every path issues the same loads.
@@ -679,7 +691,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   // global_load saddr form.  A offsets depend on the tile's row count (rows past it repeat
   // the last row) and are kept for the current and the next tile.
   const uint32_t b_off = (uint32_t)((lrow * K + lk) * 2);
-  const uint32_t q_off = (uint32_t)(lrow * (K / 2) + lk / 2);
+  const uint32_t q_off = (uint32_t)(lrow * (K / 2) + lk);
   const uint32_t s_off = (uint32_t)(lrow * (QR ? 1 : K / 128) * 2);
   // A rows: up: x[perm[arow0 + r] / k] (routed) or x[arow0 + r] (shared); down:
   // act[arow0 + r].  Rows past the tile's count repeat its last row.  The perm entries of
@@ -718,9 +730,9 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
 #pragma unroll
     for (int nb = 0; nb < kPNB; ++nb) {
       if constexpr (Q4) {
-        const char* qr = gaddr(nx ? nxt.q[nb] : cur.q[nb], (size_t)k0 / 2);
-        qreg[slot][nb][0] = gld4(qr, q_off);
-        qreg[slot][nb][1] = gld4(qr + 16, q_off);
+        const u32x2 qw = gld8(gaddr(nx ? nxt.q[nb] : cur.q[nb], (size_t)k0 / 2), q_off);
+        qreg[slot][nb][0] = qw.x;
+        qreg[slot][nb][1] = qw.y;
         // The 32-bit word holding this stage's scale (table entries are 16-byte aligned
         // and K / 128 is even here); multiply() takes its half.  QR: the row's one fp16
         // scale, reloaded each stage so the stage's load count stays the same.
@@ -733,11 +745,11 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
       }
     }
   };
-  // Wait for B slot bs (issued kPB - 1 iterations and one A group before): at most the
-  // loads of the kPB - 1 later iterations and this iteration's A loads stay outstanding.
+  // Wait for B slot bs (issued kB - 1 iterations and one A group before): at most the
+  // loads of the kB - 1 later iterations and this iteration's A loads stay outstanding.
   // The registers pass through the asm, so nothing reads them before the wait.
   auto wait_b = [&](int bs) {
-    constexpr int n = (kPB - 1) * (kPLoads + 2 * kPNB + (Q4 ? kPNB : 0)) + kPLoads;
+    constexpr int n = (kB - 1) * (kPLoads + 2 * kPNB) + kPLoads;
     static_assert(n < 64, "vmcnt range");
     if constexpr (Q4) {
       asm volatile("s_waitcnt vmcnt(%4)"
@@ -750,11 +762,11 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
                    : "n"(n));
     }
   };
-  // Stage 8 c + u (A slot u, B slot u % kPB) takes scale 4 c + u / 2: the high half of its
+  // Stage 8 c + u (A slot u, B slot u % kB) takes scale 4 c + u / 2: the high half of its
   // word for u = 2, 3, 6, 7.
   auto multiply = [&](int u) {
     const u32x4* la = slots[u];
-    const int bs = u % kPB;
+    const int bs = u % kB;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8_t b[kPNB];
@@ -788,7 +800,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   // The dequantised values are dequant_frag's, bit for bit.
   auto mma_q4 = [&](int u, int ks, const u32x4 (&cur_b)[kPNB], int nu, int nks, u32x4 (&nxt_b)[kPNB]) {
     const u32x4* lh = slots[u] + (ks ? a_rd1 : a_rd0);
-    const int ns = nu % kPB;
+    const int ns = nu % kB;
     bf16x8_t bc[kPNB];
 #pragma unroll
     for (int nb = 0; nb < kPNB; ++nb) bc[nb] = as_bf16x8(cur_b[nb]);
@@ -836,7 +848,7 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   // visible, and every wave is done reading the slot that the next stage refills.
   // (__syncthreads' release fence would wait for every outstanding load, vmcnt(0), to
   // cover the LDS writes of the direct loads.)
-  constexpr int kOpsPerStage = kPLoads + 2 * kPNB + (Q4 ? kPNB : 0);
+  constexpr int kOpsPerStage = kPLoads + 2 * kPNB;   // A, then B (int4: kPNB packed + kPNB scale loads)
   static_assert((kPA - 1) * kOpsPerStage < 64, "vmcnt range");
   auto barrier_raw = [&]() {
     asm volatile("" ::: "memory");
@@ -907,20 +919,20 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
   a_offsets(a_off_cur, pv_cur, cur);
   a_offsets(a_off_nxt, pv_nxt, nxt);
   // Prologue: the kPR iterations before stage 0, in the loop's own issue order (iteration
-  // v - kPR requests A stage v - 1 and B stage v - kPB), so the loads in flight at the top
+  // v - kPR requests A stage v - 1 and B stage v - kB), so the loads in flight at the top
   // of the loop stand exactly as they do after every later cycle.
 #pragma unroll
   for (int v = 0; v < kPR; ++v) {
     if (v >= 1) dma_a(v - 1, false, v - 1);
-    if (v >= kPR - kPB) load_b(v - (kPR - kPB), false, v - (kPR - kPB));
+    if (v >= kPR - kB) load_b(v - (kPR - kB), false, v - (kPR - kB));
   }
   stage_end();
-  // Int4: stage 0's B loads landed (the kPB - 1 later B stages and their A loads may still be
+  // Int4: stage 0's B loads landed (the kB - 1 later B stages and their A loads may still be
   // in flight) and its first k step's fragments formed; every later stage finds its first
   // fragments formed during the previous stage's second k step.
   u32x4 bq4[kPNB];
   if constexpr (Q4) {
-    wait_vm_regs<(kPB - 1) * kOpsPerStage>(qreg[0][0][0], qreg[0][0][1], qreg[0][1][0], qreg[0][1][1]);
+    wait_vm_regs<(kB - 1) * kOpsPerStage>(qreg[0][0][0], qreg[0][0][1], qreg[0][1][0], qreg[0][1][1]);
     asm volatile("" : "+v"(sreg[0][0]), "+v"(sreg[0][1]));
 #pragma unroll
     for (int nb = 0; nb < kPNB; ++nb) {
@@ -928,35 +940,35 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
       bq4[nb] = dequant_frag(qreg[0][nb][0], QR ? scale_f32<true>((uint16_t)sr) : __uint_as_float(sr << 16));
     }
   }
-  // Stage st of tile j (A slot st % kPR, B slot st % kPB): refill the A slot read at the
+  // Stage st of tile j (A slot st % kPR, B slot st % kB): refill the A slot read at the
   // previous stage with stage st + kPA, multiply, refill this stage's B slot with stage
-  // st + kPB; stages past the tile's end are the next tile's first ones (for the last
+  // st + kB; stages past the tile's end are the next tile's first ones (for the last
   // tile: its own first stages again, never multiplied).  K / 64 is a multiple of kPR, so
   // tiles start on a cycle boundary and every load is unconditional.
   auto cycle = [&](int st0, auto tail_tag) {
     constexpr bool kTail = decltype(tail_tag)::value;   // the tile's last cycle
 #pragma unroll
     for (int u = 0; u < kPR; ++u) {
-      const int sa = st0 + u + kPA, sb = st0 + u + kPB;
-      const bool na = kTail && u + kPA >= kPR, nb = kTail && u + kPB >= kPR;   // past the tile's end
+      const int sa = st0 + u + kPA, sb = st0 + u + kB;
+      const bool na = kTail && u + kPA >= kPR, nb = kTail && u + kB >= kPR;   // past the tile's end
       dma_a((u + kPA) % kPR, na, na ? sa - nk : sa);
       if constexpr (Q4) {
         // k step 0 (fragments formed before) forming k step 1's; then, once stage u + 1's B
-        // loads have landed (issued kPB - 1 stages ago: only the kPB - 2 later B stages with
+        // loads have landed (issued kB - 1 stages ago: only the kB - 2 later B stages with
         // their A loads and this stage's A loads may still be outstanding), k step 1 forming
         // stage u + 1's first.
         u32x4 q1[kPNB];
         mma_q4(u, 0, bq4, u, 1, q1);
-        const int n1 = (u + 1) % kPB;
-        wait_vm_regs<(kPB - 2) * kOpsPerStage + kPLoads>(qreg[n1][0][0], qreg[n1][0][1], qreg[n1][1][0],
+        const int n1 = (u + 1) % kB;
+        wait_vm_regs<(kB - 2) * kOpsPerStage + kPLoads>(qreg[n1][0][0], qreg[n1][0][1], qreg[n1][1][0],
                                                             qreg[n1][1][1]);
         asm volatile("" : "+v"(sreg[n1][0]), "+v"(sreg[n1][1]));
         mma_q4(u, 1, q1, u + 1, 0, bq4);
       } else {
-        wait_b(u % kPB);
+        wait_b(u % kB);
         multiply(u);
       }
-      load_b(u % kPB, nb, nb ? sb - nk : sb);
+      load_b(u % kB, nb, nb ? sb - nk : sb);
       stage_end();
     }
   };
