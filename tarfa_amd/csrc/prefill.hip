@@ -806,15 +806,20 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
     for (int nb = 0; nb < kPNB; ++nb) bc[nb] = as_bf16x8(cur_b[nb]);
     uint32_t lo[kPNB], hi[kPNB];
     float sc[kPNB], m8[kPNB];
+    // Chunks of at most 128 rows skip the MFMAs of the last two row blocks (all padding).
+    static_assert(kPMB == 10, "8 row blocks, then the two that chunks over 128 rows use");
+    const bool full = cur.m > 128;
     bf16x8_t a0 = as_bf16x8(lh[0]), a1 = as_bf16x8(lh[128]);
 #pragma unroll
     for (int i = 0; i < kPMB; ++i) {
       const bf16x8_t a = a0;
       a0 = a1;
       if (i + 2 < kPMB) a1 = as_bf16x8(lh[(i + 2) * 128]);
+      if (i < 8 || full) {
 #pragma unroll
-      for (int nb = 0; nb < kPNB; ++nb)
-        acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bc[nb], acc[i][nb], 0, 0, 0);
+        for (int nb = 0; nb < kPNB; ++nb)
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bc[nb], acc[i][nb], 0, 0, 0);
+      }
       if (i == 0) {
 #pragma unroll
         for (int nb = 0; nb < kPNB; ++nb) {
