@@ -3,9 +3,9 @@ layer (bf16 and int4) and the 48-layer, 194 GB resident stack decoding Zipf-rout
 
 Bars: top-k ids, the dispatch permutation, heat counters and route telemetry bit-exact
 against the oracle for every token and layer; outputs within max-abs 2e-2 and rel-L2 1e-3
-of the oracle for a seeded sample of tokens (prefill: each token's own experts combined in
-ascending expert id plus the shared expert; stack: sampled layers of every token, each fed
-the device's output of the layer before, experts in router order).
+of the oracle (prefill: a seeded sample of tokens, each token's own experts combined in
+ascending expert id plus the shared expert; stack: every layer of every token, each fed the
+device's output of the layer before, experts in router order).
 """
 import numpy as np
 import pytest
@@ -78,7 +78,8 @@ def test_prefill_t4096_full_size_layer(gpu, mode):
 def test_stack_48_layers_resident_zipf_decode(gpu):
     """The 48 full-size layers (194 GB of bf16 experts) resident in HBM; 5 consecutive tokens
     with Zipf(1.1) per-layer logits; ids of every (token, layer), heat and route telemetry
-    bit-exact, outputs of sampled layers of every token against the oracle."""
+    bit-exact; every token's output at every layer against the oracle (each layer's input is
+    the device's output of the layer before)."""
     L, NT = 48, 5
     ledger = ResidencyLedger(FULL, L, gpu)
     ledger.fill_seeded(41)
@@ -88,7 +89,6 @@ def test_stack_48_layers_resident_zipf_decode(gpu):
     x0 = seeded.make_tokens(FULL, 41, NT, device=gpu)
     ref_tel = OracleTelemetry(L)
     heat = np.zeros((L, FULL.num_experts), np.int64)
-    pick = np.random.default_rng(41)
     for t in range(NT):
         outs = []
         stack.decode(x0[t:t + 1], logits[t], per_layer_out=outs)
@@ -100,7 +100,7 @@ def test_stack_48_layers_resident_zipf_decode(gpu):
         for l in range(L):
             np.add.at(heat[l], ids_ref[l], 1)
             ref_tel.record(l, ids_ref[l].tolist(), FULL.num_experts)
-        for l in sorted({0, L - 1, *pick.choice(np.arange(1, L - 1), 2, replace=False).tolist()}):
+        for l in range(L):
             inp = f32(x0[t:t + 1]) if l == 0 else f32(outs[l - 1])
             gu, dn = expert_dicts(ledger.hbm[l][0], ledger.hbm[l][1], ids_ref[l:l + 1])
             sh = [f32(w) for w in layers[l].shared]
