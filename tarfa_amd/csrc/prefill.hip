@@ -981,7 +981,8 @@ __global__ __launch_bounds__(64 * kPW, 1) void k_grouped_gemm_p(GemmParams p) {
     for (int st0 = 0; st0 < nk - kPR; st0 += kPR) cycle(st0, std::false_type{});
     // The next tile's perm entries were fetched before this tile's first stage: the
     // nk - kPR >= kPR stage waits since then leave only the last kPA - 1 stages' loads
-    // outstanding.
+    // outstanding.  (A gathering launch therefore needs K >= 2 kPR stages; the host sends
+    // K = 512 gathers to the register-staged kernel.)
     a_offsets(a_off_nxt, pv_nxt, nxt);
     cycle(nk - kPR, std::true_type{});
     if (p.up) epilogue(cur, std::true_type{});
@@ -1489,25 +1490,33 @@ int prefill_launch(const uint16_t* x, int T, const int32_t* ids32, const int64_t
   auto gemm = [&](GemmParams g, int lo, int hi, bool routed_q4, long mchunks) {
     g.group_lo = lo;
     g.group_hi = hi;
+    // The fragment-load kernel reads a tile's gathered row indices one cycle (kPR stages)
+    // after requesting them, so an up GEMM it would run over K < 2 kPR stages (H = 512) runs
+    // on the register-staged kernel instead, with its narrower tiles.
+    const bool frag_kernel = routed_q4 || frag;
+    const bool staged = !persistent || (frag_kernel && g.up && g.K < 2 * kcyc);
+    if (persistent && staged) g.n_ntiles = g.up ? I / 64 : H / 128;
     const long grid = (mchunks * g.n_ntiles + 7) / 8 * 8;
-    if (persistent && routed_q4 && qr)
+    if (staged) {
+      if (routed_q4 && qr)
+        hipLaunchKernelGGL((k_grouped_gemm<kRing, true, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
+      else if (routed_q4)
+        hipLaunchKernelGGL((k_grouped_gemm<kRing, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
+      else
+        hipLaunchKernelGGL((k_grouped_gemm<kRing, false>), dim3((unsigned)grid), dim3(256), 0, s, g);
+    } else if (routed_q4 && qr) {
       hipLaunchKernelGGL((k_grouped_gemm_p<true, true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
-    else if (persistent && routed_q4)
+    } else if (routed_q4) {
       hipLaunchKernelGGL((k_grouped_gemm_p<true>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
-    else if (persistent && !frag && g.up && g.K % (5 * kBK) == 0)
-      hipLaunchKernelGGL((k_grouped_gemm_w<true, 5>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
-    else if (persistent && !frag && g.up)
-      hipLaunchKernelGGL((k_grouped_gemm_w<true, 4>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
-    else if (persistent && !frag)
-      hipLaunchKernelGGL((k_grouped_gemm_w<false, 4>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
-    else if (persistent)
+    } else if (frag) {
       hipLaunchKernelGGL((k_grouped_gemm_p<false>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
-    else if (routed_q4 && qr)
-      hipLaunchKernelGGL((k_grouped_gemm<kRing, true, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
-    else if (routed_q4)
-      hipLaunchKernelGGL((k_grouped_gemm<kRing, true>), dim3((unsigned)grid), dim3(256), 0, s, g);
-    else
-      hipLaunchKernelGGL((k_grouped_gemm<kRing, false>), dim3((unsigned)grid), dim3(256), 0, s, g);
+    } else if (g.up && g.K % (5 * kBK) == 0) {
+      hipLaunchKernelGGL((k_grouped_gemm_w<true, 5>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    } else if (g.up) {
+      hipLaunchKernelGGL((k_grouped_gemm_w<true, 4>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    } else {
+      hipLaunchKernelGGL((k_grouped_gemm_w<false, 4>), dim3(pgrid), dim3(64 * kPW), 0, s, g);
+    }
   };
   GemmParams up{};
   up.a = x; up.K = H; up.gather = 1; up.offsets = offsets; up.perm = perm; up.tile_start = tile_start;
