@@ -1,11 +1,12 @@
 """The prefill GEMMs' load pipeline is inline asm: the compiler does not know that an asm
 load's destination registers fill in later, so a copy or other use of them that it places
 before the kernel's explicit `s_waitcnt vmcnt` reads stale values (no error, wrong output).
-This compiles prefill.hip to gfx950 assembly (CPU only) and checks every grouped-GEMM kernel:
-no instruction touches a vector load's destination registers before the first
-`s_waitcnt vmcnt(...)` that follows the load on the straight-line path.  That wait need not
-cover the load (the kernels count their waits), so this is the conservative half of the
-rule; it is what a register-allocation copy right after a load breaks."""
+This compiles prefill.hip to gfx950 assembly (CPU only) and checks every grouped-GEMM kernel
+along each fall-through path: after a vector load, no instruction touches its destination
+registers until an `s_waitcnt vmcnt(N)` with at least N vector memory operations issued
+since the load (vector memory completes in issue order, so that wait covers it).  Paths are
+followed in program order through conditional branches (their fall-through is a real path)
+and end at an unconditional branch."""
 import os
 import re
 import shutil
@@ -32,7 +33,7 @@ def _regs(text):
 
 
 def early_uses(lines):
-    """(load, first instruction touching its destination) pairs with no vmcnt wait between."""
+    """(load, first instruction touching its destination before a covering wait) pairs."""
     code = [l.split(";")[0].strip() for l in lines]
     bad = []
     for i, l in enumerate(code):
@@ -40,28 +41,37 @@ def early_uses(lines):
         if not m or "_lds" in l:
             continue
         dst = _regs(m.group(3))
+        issued = 0                       # vector memory operations issued after the load
         for l2 in code[i + 1:]:
             if l2.startswith("s_waitcnt") and "vmcnt" in l2:
-                break
-            if l2.startswith(("s_endpgm", "s_branch", "s_cbranch", "s_setpc")):
-                break
-            if not l2 or l2.startswith((".", "s_")) or l2.endswith(":"):
+                if issued >= int(re.search(r"vmcnt\((\d+)\)", l2).group(1)):
+                    break
                 continue
-            if _regs(l2.split(None, 1)[1] if " " in l2 else "") & dst:
+            if l2.startswith(("s_endpgm", "s_branch", "s_setpc")):
+                break
+            if not l2 or l2.endswith(":") or l2.startswith((".", "s_")):
+                continue
+            op, _, ops = l2.partition(" ")
+            if op.startswith(("global_", "buffer_", "flat_", "scratch_")):
+                issued += 1
+            if _regs(ops) & dst:
                 bad.append((l, l2))
                 break
     return bad
 
 
 def test_checker_flags_a_copy_before_the_wait():
-    good = ["global_load_dwordx2 v[194:195], v154, s[76:77]", "v_add_u32_e32 v5, v6, v7",
-            "s_waitcnt vmcnt(3)", "v_mov_b32_e32 v3, v194"]
-    bad = ["global_load_dwordx2 v[194:195], v154, s[76:77]", "global_load_lds_dwordx4 v206, s[2:3]",
-           "v_mov_b32_e32 v3, v194", "s_waitcnt vmcnt(0)"]
+    load = "global_load_dwordx2 v[194:195], v154, s[76:77]"
+    covered = [load, "global_load_dword v7, v1, s[0:1]", "s_waitcnt vmcnt(1)", "v_mov_b32_e32 v3, v194"]
+    early = [load, "global_load_lds_dwordx4 v206, s[2:3]", "v_mov_b32_e32 v3, v194", "s_waitcnt vmcnt(0)"]
+    short = [load, "global_load_dword v7, v1, s[0:1]", "s_waitcnt vmcnt(2)", "v_mov_b32_e32 v3, v195"]
     waw = ["global_load_dword v10, v1, s[0:1]", "v_mov_b32_e32 v10, 0", "s_waitcnt vmcnt(0)"]
-    assert early_uses(good) == []
-    assert early_uses(bad) == [(bad[0], bad[2])]
+    other = [load, "v_mov_b32_e32 v3, v196", "s_branch .LBB0_1", "v_mov_b32_e32 v3, v194"]
+    assert early_uses(covered) == []
+    assert early_uses(early) == [(load, early[2])]
+    assert early_uses(short) == [(load, short[3])]     # the wait leaves this load outstanding
     assert early_uses(waw) == [(waw[0], waw[1])]
+    assert early_uses(other) == []                     # past an unconditional branch: another path
 
 
 @pytest.mark.skipif(not shutil.which(B.HIPCC) and not os.path.exists(B.HIPCC), reason="hipcc not installed")
