@@ -244,22 +244,30 @@ def test_int4_prefill_matches_dequantised_bf16_chain(gpu, T, shared, I):
     ws.status()
 
 
-def test_int4_prefill_one_cycle_tiles(gpu):
-    """H = 512: each up-GEMM tile is a single 8-stage cycle, and at T = 4096 over 16 experts
-    (208 M-chunks x 4 N-tiles) every block walks several tiles, so the next tile's token-row
-    indices are fetched and used within one cycle; the outputs against the dequantised chain."""
+@pytest.mark.parametrize("mode", ["int4", "bf16"])
+def test_prefill_one_cycle_tiles(gpu, mode):
+    """H = I = 512: each up-GEMM tile is a single 8-stage cycle (int4: the register-staged
+    kernel takes it; bf16: the whole-line kernel's shortest K, two 4-stage cycles), and at
+    T = 4096 over 16 experts (208 M-chunks) every persistent block walks several tiles, so a
+    tile's successor is prepared within its own cycles; the outputs against the oracle's chain
+    (int4: on the dequantised weights)."""
     shape = MoEShape(512, 16, 512, 8, 0)
     T = 4096
     layer = seeded.make_layer(shape, 77, device=gpu)
-    q4 = _q4_layer(layer)
-    table = tm.expert_table_q4(*q4)
+    if mode == "int4":
+        q4 = _q4_layer(layer)
+        table = tm.expert_table_q4(*q4)
+        gq, gs, dq, ds = q4
+        gu = {e: bf16.to_f32(int4.dequant(gq[e].cpu().numpy(), u16(gs[e]))) for e in range(shape.num_experts)}
+        dn = {e: bf16.to_f32(int4.dequant(dq[e].cpu().numpy(), u16(ds[e]))) for e in range(shape.num_experts)}
+    else:
+        table = tm.expert_table(layer.gate_up, layer.down)
+        gu = {e: f32(layer.gate_up[e]) for e in range(shape.num_experts)}
+        dn = {e: f32(layer.down[e]) for e in range(shape.num_experts)}
     ws = Workspace(shape, gpu, tokens=T)
     x = seeded.make_tokens(shape, 77, T, device=gpu)
     out, ids, w = tm.moe_block(shape, x, table, ws, router_w=layer.router_w)
     torch.cuda.synchronize()
-    gq, gs, dq, ds = q4
-    gu = {e: bf16.to_f32(int4.dequant(gq[e].cpu().numpy(), u16(gs[e]))) for e in range(shape.num_experts)}
-    dn = {e: bf16.to_f32(int4.dequant(dq[e].cpu().numpy(), u16(ds[e]))) for e in range(shape.num_experts)}
     ref = moe.experts_prefill(f32(x), ids.cpu().numpy(), f32(w), gu, dn, shape.num_experts)
-    assert_close_bf16(f32(out), ref, "int4 prefill H=512 T=4096")
+    assert_close_bf16(f32(out), ref, f"{mode} prefill H=512 T=4096")
     ws.status()
