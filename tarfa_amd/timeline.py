@@ -112,8 +112,10 @@ def summarize(rec, H, I, Is, E):
     routing = None
     if b.size:
         med = lambda c: float(np.median(us(b[:, c])))  # noqa: E731
-        routing = {"blocks": int(len(b)), "poll_start_med": med(0), "logits_seen_med": med(1),
-                   "logits_seen_first": float(us(b[:, 1]).min()), "selected_med": med(4),
+        polled = bool((b[:, 1] > 0).all())   # no poll (and no stamp) when the logits are supplied
+        routing = {"blocks": int(len(b)), "poll_start_med": med(0),
+                   "logits_seen_med": med(1) if polled else None,
+                   "logits_seen_first": float(us(b[:, 1]).min()) if polled else None, "selected_med": med(4),
                    "weights_med": med(5), "resolved_med": med(2), "resolved_first": float(us(b[:, 2]).min()),
                    "poll_rounds_med": float(np.median(b[:, 3]))}
     return {"total_us": total, "waves": int(grid * 4), "entry_last_us": float(us(w[:, 0]).max()),
@@ -132,8 +134,9 @@ def format_summary(s):
                    f"{r['end_last']:>6.2f}")
     r = s.get("routing")
     if r:
-        out.append(f"routing ({r['blocks']} blocks, medians): poll start {r['poll_start_med']:.2f}, logits seen "
-                   f"{r['logits_seen_med']:.2f} (first {r['logits_seen_first']:.2f}), top-k selected "
+        seen = (f"logits seen {r['logits_seen_med']:.2f} (first {r['logits_seen_first']:.2f})"
+                if r["logits_seen_med"] is not None else "logits supplied")
+        out.append(f"routing ({r['blocks']} blocks, medians): poll start {r['poll_start_med']:.2f}, {seen}, top-k selected "
                    f"{r['selected_med']:.2f}, weights {r['weights_med']:.2f}, resolved {r['resolved_med']:.2f} "
                    f"(first {r['resolved_first']:.2f}), poll rounds {r['poll_rounds_med']:.0f}")
     out.append("weight GB/s per 1 us bin: " + " ".join(f"{v:.0f}" for v in s["gbps_per_us"]))
@@ -155,6 +158,8 @@ def main(argv=None):
     ap.add_argument("--layers", type=int, default=12, help="seeded layers rotated (4 GB of experts each)")
     ap.add_argument("--calls", type=int, default=40)
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--logits", action="store_true",
+                    help="supply each call a seeded router-logits row (as the 48-layer stack does)")
     a = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     shape = MoEShape(2560, 256, 1024, 8, 1024)
@@ -163,6 +168,7 @@ def main(argv=None):
     tables = ledger.tables if a.mode == "bf16" else ResidencyLedger.quantized_from(ledger).tables
     layers = [LayerWeights(*seeded.make_block_weights(shape, 1, l, dev)) for l in range(a.layers)]
     xs = [seeded.make_tokens(shape, 1, 16, layer=l, device=dev) for l in range(a.layers)]
+    lgs = [seeded.make_logits(shape, 2, 16, layer=l, device=dev) for l in range(a.layers)] if a.logits else None
     ws = Workspace(shape, dev)
     out = torch.empty(1, shape.hidden, dtype=torch.bfloat16, device=dev)
     fn = lib().tmoe_moe_block_bf16 if a.mode == "bf16" else lib().tmoe_moe_block_int4
@@ -174,7 +180,8 @@ def main(argv=None):
         l = s % a.layers
         ly = layers[l]
         x = xs[l][(s // a.layers) % 16]
-        st = fn(x.data_ptr(), 1, ly.router_w.data_ptr(), None, tables[l].data_ptr(),
+        lg = lgs[l][(s // a.layers) % 16].data_ptr() if lgs else None
+        st = fn(x.data_ptr(), 1, ly.router_w.data_ptr(), lg, tables[l].data_ptr(),
                 *[t.data_ptr() for t in ly.shared], shape.hidden, shape.num_experts, shape.intermediate,
                 shape.top_k, shape.shared_intermediate, out.data_ptr(), None, None, None, buf.data_ptr(),
                 buf.numel(), stream)
